@@ -1,0 +1,106 @@
+/*
+ * ttfa.h -- C ABI of the MI355X (gfx950) causal GQA FlashAttention library
+ * (libttfa.so, built from tinytrain_amd/csrc).
+ *
+ * The library replaces the launch layer of the reference's attention kernels
+ * (XinqiWan412/tinytrain, kernels/flash_attn.py).  Every entry point takes plain
+ * device pointers, sizes and a hipStream_t passed as void*; no torch types appear
+ * in the signatures.  The caller owns all memory.  The library allocates nothing,
+ * never synchronises the stream, keeps no state between calls and may be called
+ * from several host threads at once.
+ *
+ * Layout contract (kernels/flash_attn.py:220-232, 246-258):
+ *   q, o, dout, dq : [B, Hq,  T, D] contiguous, element type `dtype`
+ *   k, v, dk, dv   : [B, Hkv, T, D] contiguous, element type `dtype`
+ *   lse            : [B, Hq,  T]    contiguous fp32, natural-log logsumexp of the
+ *                    scaled scores, lse = m + ln(l) (kernels/flash_attn.py:67)
+ *   delta_ws       : [B, Hq,  T]    fp32 workspace, rowsum(O * dO)
+ *                    (kernels/flash_attn.py:70-90, 255)
+ * Causal mask always on; query head h reads KV head h / (Hq / Hkv)
+ * (kernels/flash_attn.py:24, 227); the caller passes scale = 1/sqrt(D)
+ * (kernels/flash_attn.py:237, 257).
+ *
+ * Supported: dtype TTFA_BF16 or TTFA_F32, D in {64, 128}, T >= 1, Hq % Hkv == 0,
+ * all pointers non-null and 16-byte aligned.
+ *
+ * Return value: 0 on success; a negative TTFA_E* code when validation fails
+ * (checked before any HIP call, so argument errors are testable without a GPU);
+ * a positive hipError_t when a launch fails.  ttfa_strerror() names both kinds.
+ */
+#ifndef TTFA_H
+#define TTFA_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTFA_ABI_VERSION 1
+
+enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
+
+enum ttfa_status {
+  TTFA_OK = 0,
+  TTFA_E_NULL = -1,        /* a required pointer is NULL                         */
+  TTFA_E_HEAD_DIM = -2,    /* D is not 64 or 128                                 */
+  TTFA_E_GROUP = -3,       /* Hq % Hkv != 0, or Hq < 1, Hkv < 1                  */
+  TTFA_E_SEQ = -4,         /* T < 1, B < 1, or element counts overflow int64     */
+  TTFA_E_ALIGN = -5,       /* a pointer is not 16-byte aligned                   */
+  TTFA_E_DTYPE = -6,       /* dtype is not a ttfa_dtype                          */
+  TTFA_E_SCALE = -7,       /* scale is not finite and positive                   */
+};
+
+/* Library ABI version (TTFA_ABI_VERSION of the build). No reference counterpart. */
+int ttfa_abi_version(void);
+
+/* Static description of a status code (negative: validation, positive: hipError_t).
+ * No reference counterpart. */
+const char *ttfa_strerror(int code);
+
+/*
+ * Forward: o = softmax(q k^T * scale, causal) v and lse, for every (b, hq).
+ * Replaces _forward + fwd_kernel, kernels/flash_attn.py:220-243 and :12-67.
+ */
+int ttfa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+             int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
+             void *hip_stream);
+
+/*
+ * Backward: dq, dk, dv from q, k, v, o, dout and the forward's lse.  Writes
+ * delta_ws = rowsum(o * dout) first (it is recomputed on every call, never read
+ * from a previous one).  dk/dv are reduced over the Hq/Hkv query heads of each KV
+ * head inside one workgroup, without atomics, so results are bitwise reproducible.
+ * Replaces _backward + bwd_preprocess + bwd_dkdv_kernel + bwd_dq_kernel,
+ * kernels/flash_attn.py:246-277, :70-90, :93-159, :162-217.
+ */
+int ttfa_bwd(const void *q, const void *k, const void *v, const void *o,
+             const void *dout, const float *lse, float *delta_ws, void *dq,
+             void *dk, void *dv, int B, int Hq, int Hkv, int T, int D, int dtype,
+             float scale, void *hip_stream);
+
+/*
+ * The two launches ttfa_bwd is made of, exported separately so a caller (or a
+ * profiler) can run or time each pass on its own.  ttfa_bwd == ttfa_bwd_dq then
+ * ttfa_bwd_dkdv on the same stream.
+ *
+ * ttfa_bwd_dq: writes delta_ws = rowsum(o * dout) and dq.
+ *   Replaces bwd_preprocess + bwd_dq_kernel (kernels/flash_attn.py:70-90, :162-217)
+ *   and their launches (:260-261, :271-275).
+ * ttfa_bwd_dkdv: reads delta_ws (as written by ttfa_bwd_dq for the same o, dout)
+ *   and writes dk, dv.
+ *   Replaces bwd_dkdv_kernel (kernels/flash_attn.py:93-159) and its launch (:264-268).
+ */
+int ttfa_bwd_dq(const void *q, const void *k, const void *v, const void *o,
+                const void *dout, const float *lse, float *delta_ws, void *dq,
+                int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
+                void *hip_stream);
+
+int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                  const float *lse, const float *delta_ws, void *dk, void *dv,
+                  int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
+                  void *hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTFA_H */

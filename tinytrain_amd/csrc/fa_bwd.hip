@@ -1,0 +1,373 @@
+// Causal GQA FlashAttention backward, bf16 in / fp32 accumulate, gfx950.
+//
+// Two passes, both recomputing P from the forward's LSE (kernels/flash_attn.py:143-145,
+// :208-209) instead of storing it:
+//
+//  1. dQ pass (reference: bwd_preprocess :70-90 fused with bwd_dq_kernel :162-217).
+//     One workgroup = 128 query rows of one (batch, head), 4 waves x 32 rows, longest
+//     rows first.  The prologue computes Delta = rowsum(O * dO) for the workgroup's
+//     own rows from the same registers that hold dO, and writes it to the workspace
+//     for pass 2 (so there is no separate preprocess launch and dO is read once here).
+//     Per 64-key tile from LDS:  S^T = K Q^T, dP^T = V dO^T (Q and dO rows held in
+//     registers as B operands), P^T = exp2(S^T*scale*log2e - LSE*log2e),
+//     dS^T = P^T (dP^T - Delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
+//     Every lane owns one query row, so LSE and Delta are per-lane scalars.
+//
+//  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  One workgroup = 128 keys of one
+//     (batch, kv head), 4 waves x 32 keys; the wave's K and V rows stay in registers.
+//     The workgroup walks the G query heads of its group and, for each, the 64-row Q
+//     tiles from the diagonal to the end, double-buffered through LDS; dK and dV
+//     accumulate in registers across the whole group, so the group reduction needs no
+//     atomics and the result is bitwise deterministic (reference loop :125-152).
+//     Per wave and 32-row block:  S = Q K^T, dP = dO V^T (lane = key), P, dS, then
+//     dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed from LDS.
+//     dK is scaled once at the end (:154).
+#include "fa_common.h"
+#include "fa_kernels.h"
+
+namespace ttfa {
+
+// ---------------------------------------------------------------- pass 1: Delta + dQ
+template <int D>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
+    float scale_log2, float scale) {
+  constexpr int BM = 128, BN = 64;
+  constexpr int KK = D / 16, DB = D / 32, CH = D / 8, LOADS = BN * CH / 256;
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  bf16 *const lds = smem;  // [stage 2][K|V][BN*D]
+
+  const int n_tiles = (T + BM - 1) / BM;
+  const TileOrder to = order_tiles(blockIdx.x, n_tiles, B, Hq, Hkv);
+  const int qt = n_tiles - 1 - to.tile;
+  const int bh = to.bh;
+  const int G = Hq / Hkv;
+  const int b = bh / Hq, h = bh - b * Hq;
+  const int64_t kv_head = (int64_t)b * Hkv + h / G;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, lg = lane >> 5;
+  const int q0 = qt * BM + wave * 32;
+  const int qrow = q0 + lq;
+
+  const uint32_t head_bytes = (uint32_t)T * D * 2;
+  const int64_t qbase = (int64_t)bh * T * D;
+  const auto rq = make_rsrc(Q + qbase, head_bytes);
+  const auto ro = make_rsrc(O + qbase, head_bytes);
+  const auto rdo = make_rsrc(dO + qbase, head_bytes);
+  const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
+  const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
+
+  bf16x8 qf[KK], dof[KK];
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2;
+    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
+    dof[kk] = __builtin_bit_cast(bf16x8, buf_load16(rdo, off));
+    const bf16x8 of = __builtin_bit_cast(bf16x8, buf_load16(ro, off));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[s]), bf2f(dof[kk][s]), dpart);
+  }
+  const float delta = xhalf_sum(dpart);
+  float lse_t = 0.f;
+  if (qrow < T) {
+    lse_t = LSE[(int64_t)bh * T + qrow] * kLog2e;
+    if (lg == 0) Delta[(int64_t)bh * T + qrow] = delta;
+  }
+
+  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
+  u32x4 kreg[LOADS], vreg[LOADS];
+  auto load_tile = [&](int j) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
+      const uint32_t off = (uint32_t)((j * BN + row) * D + ch * 8) * 2;
+      kreg[i] = buf_load16(rk, off);
+      vreg[i] = buf_load16(rv, off);
+    }
+  };
+  auto store_tile = [&](int stage) {
+    bf16 *Kt = lds + stage * 2 * BN * D, *Vt = Kt + BN * D;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
+      const int off = row * D + (swz(row, ch) << 3);
+      *reinterpret_cast<u32x4 *>(Kt + off) = kreg[i];
+      *reinterpret_cast<u32x4 *>(Vt + off) = vreg[i];
+    }
+  };
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int j = 0; j < n_kv; ++j) {
+    if (j + 1 < n_kv) load_tile(j + 1);
+    const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
+    const int k0 = j * BN;
+    if (k0 <= q0 + 31) {
+      f32x16 s[2], dp[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        s[kb] = f32x16{};
+        dp[kb] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          s[kb] = mfma32(lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg), qf[kk], s[kb]);
+          dp[kb] = mfma32(lds_read_row8<D>(Vt, kb * 32 + lq, 2 * kk + lg), dof[kk], dp[kb]);
+        }
+      }
+      const bool masked = (k0 + BN - 1 > q0) || (k0 + BN > T);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = exp2f_fast(__builtin_fmaf(s[kb][r], scale_log2, -lse_t));
+          if (masked) {
+            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+            if (key > qrow || key >= T) p = 0.f;
+          }
+          s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
+        }
+#pragma unroll
+      for (int m = 0; m < BN / 16; ++m) {
+        const bf16x8 dsb = pack8(s[m >> 1], 8 * (m & 1));
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          dqacc[db] = mfma32(lds_read_trT<D>(Kt, 16 * m, 32 * db, lane), dsb, dqacc[db]);
+      }
+    }
+    if (j + 1 < n_kv) store_tile((j + 1) & 1);
+    __syncthreads();
+  }
+
+  if (qrow < T) {
+    bf16 *row = dQ + ((int64_t)bh * T + qrow) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *reinterpret_cast<bf16x4 *>(row + 32 * db + 8 * a + 4 * lg) =
+            pack4(dqacc[db][4 * a] * scale, dqacc[db][4 * a + 1] * scale,
+                  dqacc[db][4 * a + 2] * scale, dqacc[db][4 * a + 3] * scale);
+  }
+}
+
+// ---------------------------------------------------------------- pass 2: dK, dV
+template <int D>
+__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
+    int Hq, int Hkv, int T, float scale_log2, float scale) {
+  constexpr int BNK = 128, BMQ = 64;
+  constexpr int KK = D / 16, DB = D / 32, CH = D / 8, LOADS = BMQ * CH / 256;
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  // [stage 2][Q|dO][BMQ*D] bf16, then [stage 2][LSE*log2e | Delta][BMQ] fp32
+  bf16 *const lds = smem;
+  float *const ldsf = reinterpret_cast<float *>(smem + 2 * 2 * BMQ * D);
+
+  const int n_ktiles = (T + BNK - 1) / BNK;
+  const TileOrder to = order_tiles(blockIdx.x, n_ktiles, B, Hkv, Hkv);
+  const int kt = to.tile;  // tile 0 sees the most query rows: longest first
+  const int bhk = to.bh;   // batch * Hkv + kv head
+  const int G = Hq / Hkv;
+  const int b = bhk / Hkv, hk = bhk - b * Hkv;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 31, lg = lane >> 5;
+  const int k0w = kt * BNK + wave * 32;  // first key of this wave
+  const int krow = k0w + lq;
+
+  const uint32_t head_bytes = (uint32_t)T * D * 2;
+  const int64_t kvbase = (int64_t)bhk * T * D;
+  const auto rk = make_rsrc(K + kvbase, head_bytes);
+  const auto rv = make_rsrc(V + kvbase, head_bytes);
+
+  // K^T, V^T as B operands: lane (key lq, lg) slot s of step kk = row krow, d = 16kk+8lg+s.
+  bf16x8 kf[KK], vf[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const uint32_t off = (uint32_t)(krow * D + 16 * kk + 8 * lg) * 2;
+    kf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rk, off));
+    vf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rv, off));
+  }
+
+  const int n_qt = (T + BMQ - 1) / BMQ;
+  const int qt_lo = kt * (BNK / BMQ);
+  const int per_g = n_qt - qt_lo;
+  const int n_items = G * per_g;
+
+  u32x4 qreg[LOADS], doreg[LOADS];
+  float fl = 0.f;  // one LSE*log2e or Delta value for threads < 128
+  auto load_item = [&](int it) {
+    const int g = it / per_g, qt = qt_lo + it % per_g;
+    const int64_t bhq = (int64_t)b * Hq + hk * G + g;
+    const auto rq = make_rsrc(Q + bhq * T * D, head_bytes);
+    const auto rdo = make_rsrc(dO + bhq * T * D, head_bytes);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
+      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + ch * 8) * 2;
+      qreg[i] = buf_load16(rq, off);
+      doreg[i] = buf_load16(rdo, off);
+    }
+    if (tid < 2 * BMQ) {
+      const int r = qt * BMQ + (tid & (BMQ - 1));
+      fl = 0.f;
+      if (r < T) fl = tid < BMQ ? LSE[bhq * T + r] * kLog2e : Delta[bhq * T + r];
+    }
+  };
+  auto store_item = [&](int stage) {
+    bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
+      const int off = row * D + (swz(row, ch) << 3);
+      *reinterpret_cast<u32x4 *>(Qt + off) = qreg[i];
+      *reinterpret_cast<u32x4 *>(dOt + off) = doreg[i];
+    }
+    if (tid < 2 * BMQ) ldsf[stage * 2 * BMQ + tid] = fl;
+  };
+
+  f32x16 dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dkacc[db] = f32x16{};
+    dvacc[db] = f32x16{};
+  }
+
+  if (n_items > 0) {
+    load_item(0);
+    store_item(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < n_items; ++it) {
+    if (it + 1 < n_items) load_item(it + 1);
+    const int stage = it & 1;
+    const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
+    const float *lse_t = ldsf + stage * 2 * BMQ, *dl = lse_t + BMQ;
+    const int qt = qt_lo + it % per_g;
+#pragma unroll
+    for (int qb = 0; qb < BMQ / 32; ++qb) {
+      const int qbase = qt * BMQ + qb * 32;
+      if (qbase + 31 < k0w) continue;  // every row of the block precedes every key
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        s = mfma32(lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg), kf[kk], s);
+        dp = mfma32(lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg), vf[kk], dp);
+      }
+      const bool masked = (qbase < k0w + 31) || (qbase + 31 >= T);
+      f32x16 ds;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int rl = qb * 32 + 8 * a + 4 * lg;  // local row of register 4a
+        const f32x4 lv = *reinterpret_cast<const f32x4 *>(lse_t + rl);
+        const f32x4 dv4 = *reinterpret_cast<const f32x4 *>(dl + rl);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * a + e;
+          float p = exp2f_fast(__builtin_fmaf(s[r], scale_log2, -lv[e]));
+          if (masked) {
+            const int qr = qt * BMQ + rl + e;
+            if (krow > qr || qr >= T) p = 0.f;
+          }
+          s[r] = p;
+          ds[r] = p * (dp[r] - dv4[e]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const bf16x8 pb = pack8(s, 8 * m);
+        const bf16x8 dsb = pack8(ds, 8 * m);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          dvacc[db] = mfma32(lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane), pb, dvacc[db]);
+          dkacc[db] = mfma32(lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane), dsb, dkacc[db]);
+        }
+      }
+    }
+    if (it + 1 < n_items) store_item((it + 1) & 1);
+    __syncthreads();
+  }
+
+  if (krow < T) {
+    bf16 *dkrow = dK + kvbase + (int64_t)krow * D;
+    bf16 *dvrow = dV + kvbase + (int64_t)krow * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d = 32 * db + 8 * a + 4 * lg;
+        *reinterpret_cast<bf16x4 *>(dkrow + d) =
+            pack4(dkacc[db][4 * a] * scale, dkacc[db][4 * a + 1] * scale,
+                  dkacc[db][4 * a + 2] * scale, dkacc[db][4 * a + 3] * scale);
+        *reinterpret_cast<bf16x4 *>(dvrow + d) =
+            pack4(dvacc[db][4 * a], dvacc[db][4 * a + 1], dvacc[db][4 * a + 2], dvacc[db][4 * a + 3]);
+      }
+  }
+}
+
+template <typename Kern>
+static hipError_t allow_lds(Kern kern, size_t bytes) {
+  // Idempotent; needed once per kernel for more than 64 KiB of dynamic LDS.
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+hipError_t launch_bwd_dq_bf16(const void *q, const void *k, const void *v, const void *o,
+                              const void *dout, const float *lse, float *delta, void *dq,
+                              int B, int Hq, int Hkv, int T, int D, float scale,
+                              hipStream_t stream) {
+  const int n_tiles = (T + 127) / 128;
+  const dim3 grid((unsigned)(n_tiles * B * Hq)), block(256);
+  const float sl2 = scale * kLog2e;
+  const size_t lds = (size_t)2 * 2 * 64 * D * 2;
+  if (D == 64) {
+    auto kern = fa_bwd_dq_bf16_kernel<64>;
+    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                       (const bf16 *)o, (const bf16 *)dout, lse, delta,
+                                       (bf16 *)dq, B, Hq, Hkv, T, sl2, scale);
+  } else {
+    auto kern = fa_bwd_dq_bf16_kernel<128>;
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                       (const bf16 *)o, (const bf16 *)dout, lse, delta,
+                                       (bf16 *)dq, B, Hq, Hkv, T, sl2, scale);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkdv_bf16(const void *q, const void *k, const void *v, const void *dout,
+                                const float *lse, const float *delta, void *dk, void *dv,
+                                int B, int Hq, int Hkv, int T, int D, float scale,
+                                hipStream_t stream) {
+  const int n_ktiles = (T + 127) / 128;
+  const dim3 grid((unsigned)(n_ktiles * B * Hkv)), block(256);
+  const float sl2 = scale * kLog2e;
+  const size_t lds = (size_t)2 * 2 * 64 * D * 2 + 2 * 2 * 64 * 4;
+  if (D == 64) {
+    auto kern = fa_bwd_dkdv_bf16_kernel<64>;
+    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                       (const bf16 *)dout, lse, delta, (bf16 *)dk,
+                                       (bf16 *)dv, B, Hq, Hkv, T, sl2, scale);
+  } else {
+    auto kern = fa_bwd_dkdv_bf16_kernel<128>;
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                       (const bf16 *)dout, lse, delta, (bf16 *)dk,
+                                       (bf16 *)dv, B, Hq, Hkv, T, sl2, scale);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ttfa

@@ -1,0 +1,31 @@
+// Host-side launchers of the attention kernels (one per kernel family and dtype).
+// Arguments are validated by the C ABI layer (ttfa_api.hip) before these run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace ttfa {
+
+hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
+                           int B, int Hq, int Hkv, int T, int D, float scale, hipStream_t stream);
+hipError_t launch_bwd_dq_bf16(const void *q, const void *k, const void *v, const void *o,
+                              const void *dout, const float *lse, float *delta, void *dq,
+                              int B, int Hq, int Hkv, int T, int D, float scale,
+                              hipStream_t stream);
+hipError_t launch_bwd_dkdv_bf16(const void *q, const void *k, const void *v, const void *dout,
+                                const float *lse, const float *delta, void *dk, void *dv,
+                                int B, int Hq, int Hkv, int T, int D, float scale,
+                                hipStream_t stream);
+
+hipError_t launch_fwd_f32(const void *q, const void *k, const void *v, void *o, float *lse,
+                          int B, int Hq, int Hkv, int T, int D, float scale, hipStream_t stream);
+hipError_t launch_bwd_dq_f32(const void *q, const void *k, const void *v, const void *o,
+                             const void *dout, const float *lse, float *delta, void *dq,
+                             int B, int Hq, int Hkv, int T, int D, float scale,
+                             hipStream_t stream);
+hipError_t launch_bwd_dkdv_f32(const void *q, const void *k, const void *v, const void *dout,
+                               const float *lse, const float *delta, void *dk, void *dv,
+                               int B, int Hq, int Hkv, int T, int D, float scale,
+                               hipStream_t stream);
+
+}  // namespace ttfa

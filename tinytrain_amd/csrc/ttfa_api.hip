@@ -1,0 +1,115 @@
+// C ABI of libttfa.so: argument validation and dispatch (declarations in include/ttfa.h).
+//
+// Validation runs before any HIP call, so every argument error is reported without a
+// GPU (and without touching the HIP runtime).  Launch failures come back as the
+// positive hipError_t of hipGetLastError().
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/ttfa.h"
+#include "fa_kernels.h"
+
+namespace {
+
+int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, float scale) {
+  if (dtype != TTFA_BF16 && dtype != TTFA_F32) return TTFA_E_DTYPE;
+  if (D != 64 && D != 128) return TTFA_E_HEAD_DIM;
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return TTFA_E_GROUP;
+  if (B < 1 || T < 1) return TTFA_E_SEQ;
+  // Per-head byte extents must fit the 32-bit buffer descriptors used by the kernels,
+  // and total element counts must fit int64 with margin.
+  const int64_t esz = dtype == TTFA_BF16 ? 2 : 4;
+  if ((int64_t)T * D * esz > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if ((int64_t)B * Hq > (int64_t)0x7fffffff / 4) return TTFA_E_SEQ;
+  if ((int64_t)B * Hq * ((T + 127) / 128) > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if (!(scale > 0.f) || !isfinite(scale)) return TTFA_E_SCALE;
+  return TTFA_OK;
+}
+
+int check_ptrs(const void *const *ptrs, int n) {
+  for (int i = 0; i < n; ++i)
+    if (ptrs[i] == nullptr) return TTFA_E_NULL;
+  for (int i = 0; i < n; ++i)
+    if (reinterpret_cast<uintptr_t>(ptrs[i]) & 15u) return TTFA_E_ALIGN;
+  return TTFA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ttfa_abi_version(void) { return TTFA_ABI_VERSION; }
+
+const char *ttfa_strerror(int code) {
+  switch (code) {
+    case TTFA_OK: return "success";
+    case TTFA_E_NULL: return "ttfa: a required pointer is NULL";
+    case TTFA_E_HEAD_DIM: return "ttfa: head dim D must be 64 or 128";
+    case TTFA_E_GROUP: return "ttfa: Hq must be a positive multiple of Hkv";
+    case TTFA_E_SEQ: return "ttfa: B and T must be >= 1 and sizes must fit the kernels' index range";
+    case TTFA_E_ALIGN: return "ttfa: every pointer must be 16-byte aligned";
+    case TTFA_E_DTYPE: return "ttfa: dtype must be TTFA_BF16 or TTFA_F32";
+    case TTFA_E_SCALE: return "ttfa: scale must be finite and > 0";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "ttfa: unknown status code";
+}
+
+int ttfa_fwd(const void *q, const void *k, const void *v, void *o, float *lse, int B, int Hq,
+             int Hkv, int T, int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, o, lse};
+  if ((rc = check_ptrs(ptrs, 5))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hip_stream);
+  hipError_t e = dtype == TTFA_BF16
+                     ? ttfa::launch_fwd_bf16(q, k, v, o, lse, B, Hq, Hkv, T, D, scale, s)
+                     : ttfa::launch_fwd_f32(q, k, v, o, lse, B, Hq, Hkv, T, D, scale, s);
+  return static_cast<int>(e);
+}
+
+int ttfa_bwd_dq(const void *q, const void *k, const void *v, const void *o, const void *dout,
+                const float *lse, float *delta_ws, void *dq, int B, int Hq, int Hkv, int T,
+                int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, o, dout, lse, delta_ws, dq};
+  if ((rc = check_ptrs(ptrs, 8))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hip_stream);
+  hipError_t e =
+      dtype == TTFA_BF16
+          ? ttfa::launch_bwd_dq_bf16(q, k, v, o, dout, lse, delta_ws, dq, B, Hq, Hkv, T, D, scale, s)
+          : ttfa::launch_bwd_dq_f32(q, k, v, o, dout, lse, delta_ws, dq, B, Hq, Hkv, T, D, scale, s);
+  return static_cast<int>(e);
+}
+
+int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                  const float *lse, const float *delta_ws, void *dk, void *dv, int B, int Hq,
+                  int Hkv, int T, int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, dout, lse, delta_ws, dk, dv};
+  if ((rc = check_ptrs(ptrs, 8))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hip_stream);
+  hipError_t e =
+      dtype == TTFA_BF16
+          ? ttfa::launch_bwd_dkdv_bf16(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, scale, s)
+          : ttfa::launch_bwd_dkdv_f32(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, scale, s);
+  return static_cast<int>(e);
+}
+
+int ttfa_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
+             const float *lse, float *delta_ws, void *dq, void *dk, void *dv, int B, int Hq,
+             int Hkv, int T, int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, o, dout, lse, delta_ws, dq, dk, dv};
+  if ((rc = check_ptrs(ptrs, 10))) return rc;
+  rc = ttfa_bwd_dq(q, k, v, o, dout, lse, delta_ws, dq, B, Hq, Hkv, T, D, dtype, scale, hip_stream);
+  if (rc) return rc;
+  return ttfa_bwd_dkdv(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
+                       hip_stream);
+}
+
+}  // extern "C"
