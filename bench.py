@@ -1,0 +1,281 @@
+"""Benchmark of the causal GQA FlashAttention hot path on one MI355X.
+
+One step = forward + backward of the attention op on one batch of the workload:
+``ttfa_fwd`` then ``ttfa_bwd_dq`` then ``ttfa_bwd_dkdv`` (the three launches
+``ttfa_fwd`` + ``ttfa_bwd`` make), called through the C ABI on preallocated device
+buffers on torch's current stream.  The default workload is C2, the 112M pretrain
+attention shape (B=16, Hq=Hkv=12, T=1024, D=64, bf16), the configuration the headline
+metric is quoted on.
+
+FLOPs follow the FlashAttention convention with the causal half counted:
+fwd = 2*B*Hq*T^2*D, bwd = 2.5*fwd, step = 3.5*fwd.
+
+Inputs rotate over several resident sets (more than 512 MB in total) so the 256 MB
+last-level cache does not hold one step's operands from the previous step.
+
+Prints ONE JSON line on stdout.  ``--gpus`` above 1 is refused: this build runs on one
+GPU, and the attention op needs no collective (each (batch, kv-head) is independent).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _cpu_baseline(cfg, budget_s: float) -> dict:
+    """Oracle (repeat_interleave + SDPA, fp32, fwd + autograd bwd) on the host CPU.
+
+    Runs on leading batch slices of the same seeded workload; the slice size is
+    chosen so one repetition takes about a second, and repetitions continue until
+    ``budget_s`` seconds of CPU work have been spent (at least 3).
+    """
+    import torch
+
+    from oracle.eager_attention import eager_attention_grads
+    from tinytrain_amd.workloads import make_inputs
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    torch.set_num_threads(threads)
+    q, k, v, do, _ = make_inputs(cfg, seed=0)
+
+    def run(b: int) -> float:
+        t0 = time.perf_counter()
+        eager_attention_grads(q[:b], k[:b], v[:b], do[:b])
+        return time.perf_counter() - t0
+
+    run(1)  # warmup
+    t1 = run(1)
+    b = max(1, min(cfg.B, int(1.0 / max(t1, 1e-6))))
+    times, spent = [], 0.0
+    while spent < budget_s or len(times) < 3:
+        t = run(b)
+        times.append(t)
+        spent += t
+        if len(times) >= 50:
+            break
+    med = statistics.median(times)
+    flop = 3.5 * cfg.fwd_flop() * b / cfg.B
+    return {
+        "value": round(flop / med / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{cfg.name} batch slice b={b} of B={cfg.B} (same seeded inputs), fp32 "
+                   f"repeat_interleave + causal SDPA forward + autograd backward on the CPU, "
+                   f"median of {len(times)} runs ({spent:.1f} s of CPU work)"),
+        "seconds_per_sample": round(med, 4),
+        "cpu_model": _cpu_model(),
+        "torch_threads": torch.get_num_threads(),
+    }
+
+
+def _copy_probe(mb: float, steps: int, dev) -> int:
+    """A plain copy of known size: each launch reads and writes exactly ``mb`` MB."""
+    import torch
+
+    n = int(mb * 1e6) // 16 * 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"copy_probe_bytes": src.nbytes, "steps": steps,
+                      "GB_per_s_read_plus_write": round(2 * src.nbytes / dt / 1e9, 1)}), flush=True)
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C2", help="workload: C1..C5 (default C2)")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="input sets to rotate over (0: enough for > 512 MB)")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU work for the CPU baseline (0 disables it)")
+    ap.add_argument("--copy-probe-mb", type=float, default=0.0,
+                    help="instead of the workload, run --steps plain device copies of this "
+                         "many MB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the attention op shards by (batch, kv-head) "
+              "with no exchange, and no multi-GPU run is part of this build. Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tinytrain_amd.workloads import CONFIGS, make_inputs
+    from tinytrain_amd import _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.copy_probe_mb > 0:
+        return _copy_probe(args.copy_probe_mb, args.steps, dev)
+    cfg = CONFIGS[args.config]
+    lib = _lib.load()
+    B, Hq, Hkv, T, D = cfg.B, cfg.Hq, cfg.Hkv, cfg.T, cfg.D
+    dt_code = _lib.TTFA_BF16 if cfg.dtype == torch.bfloat16 else _lib.TTFA_F32
+    scale = 1.0 / math.sqrt(D)
+
+    q0, k0, v0, do0, _ = make_inputs(cfg, seed=0)
+    set_bytes = 2 * (q0.nbytes + do0.nbytes) + 3 * (k0.nbytes + v0.nbytes) + 2 * B * Hq * T * 4
+    nsets = args.sets or max(2, math.ceil(512e6 / set_bytes) + 1)
+    sets = []
+    for i in range(nsets):
+        if i == 0:
+            q, k, v, do = (t.to(dev) for t in (q0, k0, v0, do0))
+        else:  # perturbed copies: same statistics, different bits
+            q, k, v, do = (t.to(dev).roll(i, dims=2).contiguous() for t in (q0, k0, v0, do0))
+        o = torch.empty_like(q)
+        lse = torch.empty((B, Hq, T), device=dev, dtype=torch.float32)
+        delta = torch.empty((B * Hq, T), device=dev, dtype=torch.float32)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        sets.append((q, k, v, do, o, lse, delta, dq, dk, dv))
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    def launch(s, ev=None):
+        q, k, v, do, o, lse, delta, dq, dk, dv = s
+        if ev is not None:
+            ev[0].record(stream)
+        _lib.check(lib.ttfa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                lse.data_ptr(), B, Hq, Hkv, T, D, dt_code, scale, sp))
+        if ev is not None:
+            ev[1].record(stream)
+        _lib.check(lib.ttfa_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   do.data_ptr(), lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                   B, Hq, Hkv, T, D, dt_code, scale, sp))
+        if ev is not None:
+            ev[2].record(stream)
+        _lib.check(lib.ttfa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                     lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                     B, Hq, Hkv, T, D, dt_code, scale, sp))
+        if ev is not None:
+            ev[3].record(stream)
+
+    for i in range(args.warmup):
+        launch(sets[i % nsets])
+    torch.cuda.synchronize()
+
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(K):
+        launch(sets[i % nsets], evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(end) / K
+
+    kms = {"fwd": [], "bwd_dq": [], "bwd_dkdv": []}
+    for ev in evs:
+        kms["fwd"].append(ev[0].elapsed_time(ev[1]))
+        kms["bwd_dq"].append(ev[1].elapsed_time(ev[2]))
+        kms["bwd_dkdv"].append(ev[2].elapsed_time(ev[3]))
+    avg = {n: sum(x) / len(x) for n, x in kms.items()}
+
+    fwd_f = cfg.fwd_flop()
+    peak = PEAK_BF16_TFLOPS if cfg.dtype == torch.bfloat16 else PEAK_F32_TFLOPS
+    step_tflops = 3.5 * fwd_f / (ms_step * 1e-3) / 1e12
+    fwd_tflops = fwd_f / (avg["fwd"] * 1e-3) / 1e12
+    bwd_ms = avg["bwd_dq"] + avg["bwd_dkdv"]
+    bwd_tflops = 2.5 * fwd_f / (bwd_ms * 1e-3) / 1e12
+
+    # Dominant kernel: per causal (query row, key) pair a kernel's MFMA work is 2*D
+    # FLOPs per matmul it needs for its outputs: fwd 2 (S, O), dQ pass 3 (S, dP, dQ),
+    # dK/dV pass 4 (S, dP, dV, dK); pairs = B*Hq*T^2/2.
+    n_mm = {"fwd": 2, "bwd_dq": 3, "bwd_dkdv": 4}
+    dom = max(avg, key=avg.get)
+    kern_flop = n_mm[dom] * fwd_f / 2
+    achieved = kern_flop / (avg[dom] * 1e-3) / 1e12
+    kernel_symbol = {"fwd": "fa_fwd_bf16_kernel", "bwd_dq": "fa_bwd_dq_bf16_kernel",
+                     "bwd_dkdv": "fa_bwd_dkdv_bf16_kernel"}[dom]
+    if cfg.dtype == torch.float32:
+        kernel_symbol = kernel_symbol.replace("bf16", "f32")
+
+    line = {
+        "metric": "causal GQA FA fwd+bwd TFLOP/s & % bf16 MFMA peak on 1 MI355X",
+        "value": round(step_tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else "f32",
+        "data": "synthetic (seeded; q,k unit-RMS, v~N(0,1), dO~N(0,1)*1e-2)",
+        "config": {"workload": f"{cfg.name}: causal {'GQA' if cfg.group > 1 else 'MHA'} attention "
+                               f"fwd+bwd", "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "D": D,
+                   "input_sets_rotated": nsets},
+        "frac_of_peak": round(step_tflops / peak, 4),
+        "passes": {
+            "fwd": {"ms": round(avg["fwd"], 5), "tflops": round(fwd_tflops, 2),
+                    "frac": round(fwd_tflops / peak, 4)},
+            "bwd": {"ms": round(bwd_ms, 5), "tflops": round(bwd_tflops, 2),
+                    "frac": round(bwd_tflops / peak, 4)},
+            "bwd_dq_ms": round(avg["bwd_dq"], 5),
+            "bwd_dkdv_ms": round(avg["bwd_dkdv"], 5),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": kernel_symbol,
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "avg_launch_ms": round(avg[dom], 5),
+            "flop_per_launch": kern_flop,
+        },
+        "wall_s_timed": round(wall, 4),
+    }
+    if args.cpu_budget > 0:
+        line["cpu_baseline"] = _cpu_baseline(cfg, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

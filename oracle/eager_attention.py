@@ -215,3 +215,9 @@ def max_abs(a: Tensor, b: Tensor) -> float:
     if torch.isnan(d).any():
         return float("inf")
     return float(d.max()) if d.numel() else 0.0
+
+
+# Parity tolerances (max-abs against this oracle) from the workload specification:
+# O, dQ, dK, dV within 2e-2 for bf16 inputs and 1e-5 for fp32; LSE within 1e-3.
+TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
+TOL_LSE = 1e-3

@@ -18,7 +18,8 @@ import torch.nn.functional as F
 from helpers import announce, assert_close_abs
 from oracle.eager_attention import (attention_bwd, attention_fwd, eager_attention_grads,
                                     max_abs, reference_outputs)
-from oracle.inputs import CONFIGS, TOL, TOL_LSE, make_custom, make_inputs
+from oracle.eager_attention import TOL, TOL_LSE
+from tinytrain_amd.workloads import CONFIGS, make_custom, make_inputs
 from tinytrain_amd import _lib
 from tinytrain_amd.attention import Attention, RMSNorm, precompute_rope
 from tinytrain_amd.kernels.flash_attn import (_backward, _forward, flash_attn, flash_attn_bwd,

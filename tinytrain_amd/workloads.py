@@ -1,6 +1,7 @@
-"""Seeded synthetic inputs for the five attention workloads (TEST INFRASTRUCTURE ONLY).
+"""The five attention workloads and their seeded synthetic inputs.
 
-The same bits are produced on every host: everything is drawn on the CPU from
+Used by bench.py (the timed inputs), by the tests and by the CPU oracle's checks, so
+every consumer sees the same bits.  The same bits are produced on every host: everything is drawn on the CPU from
 ``torch.Generator("cpu").manual_seed(seed)`` in the order q, k, v, dO (the seed 0 and
 the randn-per-tensor pattern follow tests/test_flash_attn.py:16-21), then normalised,
 then cast, and only then moved to a device.
@@ -54,11 +55,6 @@ CONFIGS: Dict[str, AttnConfig] = {
     "C4": AttnConfig("C4", 4, 16, 8, 4096, 128, torch.bfloat16, "qk", 1e-2, outlier_frac=0.01),
     "C5": AttnConfig("C5", 1, 16, 8, 16384, 128, torch.bfloat16, "qk", 1e-2),
 }
-
-# Parity tolerances (max-abs) from the workload specification.
-TOL = {torch.bfloat16: 2e-2, torch.float32: 1e-5}
-TOL_LSE = 1e-3
-
 
 def unit_rms(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """x * rsqrt(mean(x^2) + eps) along the last dim, in fp32 (model.py:33-34)."""
