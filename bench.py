@@ -77,7 +77,7 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
         t = run(b)
         times.append(t)
         spent += t
-        if len(times) >= 50:
+        if len(times) >= 400:
             break
     med = statistics.median(times)
     flop = 3.5 * cfg.fwd_flop() * b / cfg.B
@@ -93,6 +93,101 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
         "cpu_model": _cpu_model(),
         "torch_threads": torch.get_num_threads(),
     }
+
+
+TRAFFIC_DIR = ROOT / "profiles"
+
+
+def _traffic_file(config: str) -> Path:
+    return TRAFFIC_DIR / f"hbm_traffic_{config}.txt"
+
+
+def _pmc_pass(counter: str, cmd: list, out_dir: Path) -> dict:
+    """One ``rocprofv3 --pmc <counter>`` pass over ``cmd`` (a child process); returns
+    {kernel symbol: mean counter value per dispatch (KiB)}."""
+    import csv
+    import subprocess
+
+    out_dir.mkdir(parents=True, exist_ok=True)
+    full = ["rocprofv3", "--pmc", counter, "-d", str(out_dir), "-o", "run",
+            "--output-format", "csv", "--", sys.executable, *cmd]
+    print("[traffic] " + " ".join(full), file=sys.stderr, flush=True)
+    with open(out_dir / "rocprofv3.log", "w") as log:
+        subprocess.run(full, check=True, timeout=180, stdout=log, stderr=subprocess.STDOUT,
+                       cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"})
+    sums: dict = {}
+    for path in out_dir.rglob("*counter_collection.csv"):
+        for row in csv.DictReader(open(path)):
+            if row["Counter_Name"] != counter:
+                continue
+            name = row["Kernel_Name"]
+            tot, n = sums.get(name, (0.0, 0))
+            sums[name] = (tot + float(row["Counter_Value"]), n + 1)
+    return {k: tot / n for k, (tot, n) in sums.items()}
+
+
+def _measure_traffic(config: str, out: Path) -> int:
+    """FETCH_SIZE and WRITE_SIZE per dispatch of each attention kernel on ``config``,
+    scaled by what the same counters read for a plain 256 MB device copy."""
+    me = str(ROOT / "bench.py")
+    work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
+            "--no-traffic"]
+    copy_mb = 256.0
+    copy = ["--copy-probe-mb", str(copy_mb), "--steps", "10"]
+    tmp = Path("/tmp") / f"ttfa_traffic_{os.getpid()}"
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        res[counter] = _pmc_pass(counter, [me, *work], tmp / f"{counter}_work")
+        res[counter + "_copy"] = _pmc_pass(counter, [me, *copy], tmp / f"{counter}_copy")
+    copy_kib = int(copy_mb * 1e6) // 16 * 16 / 1024.0
+
+    def copy_factor(counter):
+        vals = [v for k, v in res[counter + "_copy"].items() if "copyBuffer" in k or "copy" in k.lower()]
+        return copy_kib / max(vals) if vals else float("nan")
+
+    fr, fw = copy_factor("FETCH_SIZE"), copy_factor("WRITE_SIZE")
+    kernels = {}
+    for name, kib in res["FETCH_SIZE"].items():
+        if "ttfa::" not in name:
+            continue
+        sym = name.split("ttfa::", 1)[1].split("(", 1)[0]
+        wk = res["WRITE_SIZE"].get(name, float("nan"))
+        kernels[sym] = {"fetch_kib_raw": round(kib, 1), "write_kib_raw": round(wk, 1),
+                        "read_bytes": round(kib * fr * 1024), "write_bytes": round(wk * fw * 1024),
+                        "traffic_bytes": round((kib * fr + wk * fw) * 1024)}
+    summary = {"config": config, "fetch_scale": round(fr, 4), "write_scale": round(fw, 4),
+               "copy_probe_bytes": copy_kib * 1024, "kernels": kernels}
+    lines = [
+        f"# HBM traffic per dispatch, workload {config} (rocprofv3 --pmc, one counter per pass)",
+        "# command: python bench.py --measure-traffic --config " + config,
+        f"# passes: rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -- python bench.py {' '.join(work)}",
+        f"#         rocprofv3 --pmc FETCH_SIZE|WRITE_SIZE -- python bench.py {' '.join(copy)}",
+        f"# calibration: a {copy_mb:.0f} MB device copy reads FETCH_SIZE x{fr:.3f} and "
+        f"WRITE_SIZE x{fw:.3f} of its true size;",
+        "# read/write bytes below are the raw KiB scaled by those factors.",
+        f"{'kernel':<34}{'FETCH KiB':>12}{'WRITE KiB':>12}{'read MB':>10}{'write MB':>10}",
+    ]
+    for sym, r in sorted(kernels.items()):
+        lines.append(f"{sym:<34}{r['fetch_kib_raw']:>12.1f}{r['write_kib_raw']:>12.1f}"
+                     f"{r['read_bytes'] / 1e6:>10.2f}{r['write_bytes'] / 1e6:>10.2f}")
+    lines.append("JSON " + json.dumps(summary))
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines), flush=True)
+    return 0
+
+
+def _load_traffic(config: str, kernel: str):
+    """Bytes per launch of ``kernel`` from the committed PMC summary, or None."""
+    path = _traffic_file(config)
+    if not path.exists():
+        return None, None
+    for line in path.read_text().splitlines():
+        if line.startswith("JSON "):
+            rec = json.loads(line[5:]).get("kernels", {}).get(kernel)
+            if rec:
+                return rec["traffic_bytes"], str(path.relative_to(ROOT))
+    return None, None
 
 
 def _copy_probe(mb: float, steps: int, dev) -> int:
@@ -128,6 +223,12 @@ def main() -> int:
     ap.add_argument("--copy-probe-mb", type=float, default=0.0,
                     help="instead of the workload, run --steps plain device copies of this "
                          "many MB (calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--measure-traffic", action="store_true",
+                    help="run rocprofv3 FETCH_SIZE / WRITE_SIZE passes over --config and a "
+                         "plain copy, and write the per-kernel HBM traffic summary")
+    ap.add_argument("--traffic-out", default="",
+                    help="where --measure-traffic writes (default profiles/hbm_traffic_<cfg>.txt)")
+    ap.add_argument("--no-traffic", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -135,6 +236,10 @@ def main() -> int:
               "with no exchange, and no multi-GPU run is part of this build. Use --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.measure_traffic:  # parent never touches the GPU; the passes are children
+        out = Path(args.traffic_out) if args.traffic_out else _traffic_file(args.config)
+        return _measure_traffic(args.config, out)
 
     import torch
 
@@ -232,6 +337,8 @@ def main() -> int:
                      "bwd_dkdv": "fa_bwd_dkdv_bf16_kernel"}[dom]
     if cfg.dtype == torch.float32:
         kernel_symbol = kernel_symbol.replace("bf16", "f32")
+    kernel_symbol += f"<{D}>"
+    traffic, traffic_src = (None, None) if args.no_traffic else _load_traffic(cfg.name, kernel_symbol)
 
     line = {
         "metric": "causal GQA FA fwd+bwd TFLOP/s & % bf16 MFMA peak on 1 MI355X",
@@ -265,7 +372,8 @@ def main() -> int:
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "avg_launch_ms": round(avg[dom], 5),
             "flop_per_launch": kern_flop,
         },

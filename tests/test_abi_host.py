@@ -1,0 +1,226 @@
+"""CPU tests of the C ABI (libttfa.so) and the host-side op surface.
+
+No compute call runs here: the library is loaded, its exports are checked against
+include/ttfa.h, and every argument-validation path is exercised (validation returns
+before any HIP call, include/ttfa.h).  The Python side is checked for the reference's
+op names, schemas, fake shapes, autograd registration and loud failure modes
+(kernels/flash_attn.py:220-327; model.py:92-98; pretrain.py:226-231).
+"""
+
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tinytrain_amd import _lib
+from tinytrain_amd.attention import ATTN_IMPLS, causal_attention, validate_attn_impl
+from tinytrain_amd.kernels import flash_attn as fa
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ttfa.h"
+
+needs_lib = pytest.mark.skipif(not _lib.LIB_PATH.exists(),
+                               reason="libttfa.so not built (python -m tinytrain_amd.build)")
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ttfa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_python_binding():
+    assert _declared_functions() == sorted(_lib.EXPORTED)
+
+
+@needs_lib
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in ttfa.h but not exported"
+    assert _lib.load().ttfa_abi_version() == _lib.ABI_VERSION
+
+
+@needs_lib
+@pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7])
+def test_strerror_names_validation_codes(code):
+    msg = _lib.strerror(code)
+    assert msg.startswith("ttfa:") and "unknown" not in msg
+
+
+# Fake, 16-byte aligned, non-null device addresses: every call below fails validation
+# and returns before touching them or the HIP runtime.
+P = [0x100000 + 0x1000 * i for i in range(10)]
+OK = dict(B=1, Hq=4, Hkv=2, T=128, D=64, dtype=_lib.TTFA_BF16, scale=0.125)
+
+
+def _fwd(ptrs=None, **kw):
+    a = {**OK, **kw}
+    p = P[:5] if ptrs is None else ptrs
+    return _lib.load().ttfa_fwd(*p, a["B"], a["Hq"], a["Hkv"], a["T"], a["D"], a["dtype"],
+                                a["scale"], None)
+
+
+def _bwd(ptrs=None, **kw):
+    a = {**OK, **kw}
+    p = P[:10] if ptrs is None else ptrs
+    return _lib.load().ttfa_bwd(*p, a["B"], a["Hq"], a["Hkv"], a["T"], a["D"], a["dtype"],
+                                a["scale"], None)
+
+
+def _bwd_dq(ptrs=None, **kw):
+    a = {**OK, **kw}
+    p = P[:8] if ptrs is None else ptrs
+    return _lib.load().ttfa_bwd_dq(*p, a["B"], a["Hq"], a["Hkv"], a["T"], a["D"], a["dtype"],
+                                   a["scale"], None)
+
+
+def _bwd_dkdv(ptrs=None, **kw):
+    a = {**OK, **kw}
+    p = P[:8] if ptrs is None else ptrs
+    return _lib.load().ttfa_bwd_dkdv(*p, a["B"], a["Hq"], a["Hkv"], a["T"], a["D"],
+                                     a["dtype"], a["scale"], None)
+
+
+CASES = [
+    (dict(D=96), _lib.E_HEAD_DIM),
+    (dict(D=32), _lib.E_HEAD_DIM),
+    (dict(Hq=3, Hkv=2), _lib.E_GROUP),
+    (dict(Hkv=0), _lib.E_GROUP),
+    (dict(Hq=0), _lib.E_GROUP),
+    (dict(T=0), _lib.E_SEQ),
+    (dict(B=0), _lib.E_SEQ),
+    (dict(T=1 << 24), _lib.E_SEQ),          # one head's bytes exceed the 2 GiB window
+    (dict(dtype=2), _lib.E_DTYPE),
+    (dict(dtype=-1), _lib.E_DTYPE),
+    (dict(scale=0.0), _lib.E_SCALE),
+    (dict(scale=-0.1), _lib.E_SCALE),
+    (dict(scale=math.inf), _lib.E_SCALE),
+    (dict(scale=math.nan), _lib.E_SCALE),
+]
+
+
+@needs_lib
+@pytest.mark.parametrize("entry", [_fwd, _bwd, _bwd_dq, _bwd_dkdv])
+@pytest.mark.parametrize("kw, code", CASES)
+def test_argument_errors_return_codes(entry, kw, code):
+    assert entry(**kw) == code
+
+
+@needs_lib
+@pytest.mark.parametrize("entry, n", [(_fwd, 5), (_bwd, 10), (_bwd_dq, 8), (_bwd_dkdv, 8)])
+def test_null_and_misaligned_pointers(entry, n):
+    for i in range(n):
+        ptrs = list(P[:n])
+        ptrs[i] = None
+        assert entry(ptrs=ptrs) == _lib.E_NULL
+        ptrs[i] = P[i] + 8
+        assert entry(ptrs=ptrs) == _lib.E_ALIGN
+
+
+@needs_lib
+def test_check_raises_with_message():
+    with pytest.raises(_lib.TTFAError, match="head dim"):
+        _lib.check(_fwd(D=80))
+
+
+# ------------------------------------------------------------ Python op surface
+def test_custom_ops_registered_with_reference_schemas():
+    fwd = torch.ops.tinytrain.flash_attn_fwd.default
+    bwd = torch.ops.tinytrain.flash_attn_bwd.default
+    assert [a.name for a in fwd._schema.arguments] == ["q", "k", "v"]
+    assert len(fwd._schema.returns) == 2
+    assert [a.name for a in bwd._schema.arguments] == ["q", "k", "v", "o", "do", "M"]
+    assert len(bwd._schema.returns) == 3
+
+
+def test_fake_impls_and_autograd_under_fake_mode():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        q = torch.empty(2, 8, 64, 128, dtype=torch.bfloat16, requires_grad=True)
+        k = torch.empty(2, 2, 64, 128, dtype=torch.bfloat16, requires_grad=True)
+        v = torch.empty(2, 2, 64, 128, dtype=torch.bfloat16, requires_grad=True)
+        o, M = fa.flash_attn_fwd(q, k, v)
+        assert o.shape == q.shape and o.dtype == q.dtype
+        assert M.shape == (2, 8, 64) and M.dtype == torch.float32
+        o.float().sum().backward()
+        assert q.grad.shape == q.shape and k.grad.shape == k.shape and v.grad.shape == v.shape
+
+
+def test_compile_fullgraph_traces_one_opaque_node():
+    # Dynamo traces through the fake impl with fullgraph=True (a graph break would raise
+    # during tracing); the captured graph holds the custom op, never the ctypes call.
+    graphs = []
+
+    def backend(gm, example_inputs):
+        graphs.append(gm)
+        return gm.forward
+
+    def f(q, k, v):
+        return fa.flash_attn(q, k, v) * 2
+
+    q = torch.randn(1, 4, 16, 64)
+    k = torch.randn(1, 2, 16, 64)
+    cf = torch.compile(f, backend=backend, fullgraph=True)
+    with pytest.raises(fa.FlashAttnInputError, match="ROCm GPU"):
+        cf(q, k, k)  # traced, then the real op rejects CPU tensors loudly
+    assert len(graphs) == 1
+    assert "tinytrain.flash_attn_fwd" in str(graphs[0].graph)
+
+
+def _t(*s, dtype=torch.bfloat16):
+    return torch.zeros(*s, dtype=dtype)
+
+
+@pytest.mark.parametrize("q, k, v, match", [
+    (_t(1, 4, 8, 64).transpose(2, 3), _t(1, 4, 64, 8), _t(1, 4, 64, 8), "contiguous"),
+    (_t(4, 8, 64), _t(4, 8, 64), _t(4, 8, 64), "4-D"),
+    (_t(1, 4, 8, 64), _t(1, 3, 8, 64), _t(1, 3, 8, 64), "multiple"),
+    (_t(1, 4, 8, 96), _t(1, 4, 8, 96), _t(1, 4, 8, 96), "head dim"),
+    (_t(1, 4, 8, 64), _t(1, 4, 8, 64, dtype=torch.float16), _t(1, 4, 8, 64), "dtype"),
+    (_t(1, 4, 8, 64), _t(1, 2, 9, 64), _t(1, 2, 9, 64), "matching"),
+    (_t(1, 4, 8, 64), _t(1, 2, 8, 64), _t(1, 2, 8, 64), "ROCm GPU"),
+])
+def test_forward_rejects_bad_inputs_loudly(q, k, v, match):
+    with pytest.raises(fa.FlashAttnInputError, match=match):
+        fa._forward(q, k, v)
+
+
+def test_non_contiguous_is_also_an_assertion_error():
+    # The reference asserts contiguity (kernels/flash_attn.py:221-223).
+    q = _t(1, 4, 64, 8).transpose(2, 3)
+    with pytest.raises(AssertionError):
+        fa._forward(q, _t(1, 4, 8, 64), _t(1, 4, 8, 64))
+
+
+def test_attn_impl_switch_validates_names():
+    assert ATTN_IMPLS == ("sdpa", "hip")
+    assert validate_attn_impl("hip") == "hip"
+    for bad in ("triton", "flash", "", "HIP"):
+        with pytest.raises(ValueError):
+            validate_attn_impl(bad)
+
+
+def test_sdpa_branch_is_the_eager_path():
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 4, 12, 64, generator=g)
+    k = torch.randn(1, 2, 12, 64, generator=g)
+    v = torch.randn(1, 2, 12, 64, generator=g)
+    a = causal_attention(q, k, v, "sdpa", enable_gqa=False)
+    b = causal_attention(q, k, v, "sdpa", enable_gqa=True)
+    assert torch.allclose(a, b, atol=1e-6)
+
+
+def test_hip_switch_on_cpu_fails_loudly():
+    q = torch.randn(1, 2, 8, 64)
+    with pytest.raises(fa.FlashAttnInputError):
+        causal_attention(q, q, q, "hip")
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libttfa.so")
+    with pytest.raises(_lib.LibraryNotBuilt, match="missing"):
+        _lib.load()
