@@ -8,24 +8,165 @@
 //     rows first.  The prologue computes Delta = rowsum(O * dO) for the workgroup's
 //     own rows from the same registers that hold dO, and writes it to the workspace
 //     for pass 2 (so there is no separate preprocess launch and dO is read once here).
-//     Per 64-key tile from LDS:  S^T = K Q^T, dP^T = V dO^T (Q and dO rows held in
-//     registers as B operands), P^T = exp2(S^T*scale*log2e - LSE*log2e),
+//     Per key tile from LDS (64 keys for D=64, 32 for D=128):  S^T = K Q^T and
+//     dP^T - Delta = V dO^T - Delta (the dP accumulator starts at -Delta, a per-lane
+//     constant, so dS costs one multiply), P^T = exp2(S^T*scale*log2e - LSE*log2e),
 //     dS^T = P^T (dP^T - Delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
 //     Every lane owns one query row, so LSE and Delta are per-lane scalars.
 //
 //  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  One workgroup = 128 keys of one
 //     (batch, kv head), 4 waves x 32 keys; the wave's K and V rows stay in registers.
 //     The workgroup walks the G query heads of its group and, for each, the 64-row Q
-//     tiles from the diagonal to the end, double-buffered through LDS; dK and dV
-//     accumulate in registers across the whole group, so the group reduction needs no
-//     atomics and the result is bitwise deterministic (reference loop :125-152).
-//     Per wave and 32-row block:  S = Q K^T, dP = dO V^T (lane = key), P, dS, then
-//     dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed from LDS.
-//     dK is scaled once at the end (:154).
+//     tiles from the diagonal to the end, double-buffered through LDS together with the
+//     tiles' LSE*log2e and -Delta; dK and dV accumulate in registers across the whole
+//     group, so the group reduction needs no atomics and the result is bitwise
+//     deterministic (reference loop :125-152).  Per wave and 32-row block:  S = Q K^T,
+//     dP - Delta = dO V^T - Delta (accumulator initialised from the staged -Delta),
+//     P, dS, then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
+//     from LDS.  dK is scaled once at the end (:154).
+//
+// Tiles entirely above the diagonal are skipped; only tiles crossing the diagonal or
+// the ragged end of T run the masked body.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
 namespace ttfa {
+
+namespace {
+
+template <int D>
+struct DqTile {
+  static constexpr int BM = 128;                 // query rows per workgroup
+  static constexpr int BN = D == 64 ? 64 : 32;   // keys per LDS tile
+  static constexpr int KB = BN / 32;             // 32-key blocks per tile
+  static constexpr int KK = D / 16, DB = D / 32, CH = D / 8;
+  static constexpr int LOADS = BN * CH / 256;    // 16-byte loads per thread per K (or V) tile
+  static constexpr int LDS_BYTES = 2 * 2 * BN * D * 2;  // [stage][K|V] bf16
+};
+
+template <int D>
+struct DkvTile {
+  static constexpr int BNK = 128;                // keys per workgroup
+  static constexpr int BMQ = 64;                 // query rows per LDS tile
+  static constexpr int KK = D / 16, DB = D / 32, CH = D / 8;
+  static constexpr int LOADS = BMQ * CH / 256;   // 16-byte loads per thread per Q (or dO) tile
+  // [stage][Q|dO] bf16 tiles, then [stage][LSE*log2e | -Delta] fp32 rows
+  static constexpr int LDS_BYTES = 2 * 2 * BMQ * D * 2 + 2 * 2 * BMQ * 4;
+};
+
+// One key tile of the dQ pass for one wave.
+template <int D, bool MASK>
+__device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf16x8 (&qf)[D / 16],
+                                        const bf16x8 (&dof)[D / 16], const f32x16 &ndelta,
+                                        f32x16 (&dqacc)[D / 32], float lse_t, float scale_log2,
+                                        int k0, int qrow, int T, int lane) {
+  using P = DqTile<D>;
+  const int lq = lane & 31, lg = lane >> 5;
+  f32x16 s[P::KB], dp[P::KB];
+#pragma unroll
+  for (int kb = 0; kb < P::KB; ++kb) {
+    bf16x8 kf[P::KK], vf[P::KK];
+#pragma unroll
+    for (int kk = 0; kk < P::KK; ++kk) {
+      kf[kk] = lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg);
+      vf[kk] = lds_read_row8<D>(Vt, kb * 32 + lq, 2 * kk + lg);
+    }
+    s[kb] = mfma32(kf[0], qf[0], f32x16{});
+    dp[kb] = mfma32(vf[0], dof[0], ndelta);
+#pragma unroll
+    for (int kk = 1; kk < P::KK; ++kk) {
+      s[kb] = mfma32(kf[kk], qf[kk], s[kb]);
+      dp[kb] = mfma32(vf[kk], dof[kk], dp[kb]);
+    }
+  }
+#pragma unroll
+  for (int kb = 0; kb < P::KB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = __builtin_fmaf(s[kb][r], scale_log2, -lse_t);
+      if (MASK) {
+        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (key > qrow || key >= T) x = -INFINITY;
+      }
+      s[kb][r] = exp2f_fast(x) * dp[kb][r];  // dS^T = P^T (dP^T - Delta)
+    }
+#pragma unroll
+  for (int m = 0; m < P::BN / 16; ++m) {
+    const bf16x8 dsb = pack8(s[m >> 1], 8 * (m & 1));
+    bf16x8 kt[P::DB];
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) kt[db] = lds_read_trT<D>(Kt, 16 * m, 32 * db, lane);
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) dqacc[db] = mfma32(kt[db], dsb, dqacc[db]);
+  }
+}
+
+// One 32-row query block of the dK/dV pass for one wave (its 32 keys).
+template <int D, bool MASK>
+__device__ __forceinline__ void dkdv_block(const bf16 *Qt, const bf16 *dOt, const float *lse_t,
+                                           const float *nd_t, const bf16x8 (&kf)[D / 16],
+                                           const bf16x8 (&vf)[D / 16], f32x16 (&dkacc)[D / 32],
+                                           f32x16 (&dvacc)[D / 32], int qb, int qbase, int krow,
+                                           int T, float scale_log2, int lane) {
+  using P = DkvTile<D>;
+  const int lq = lane & 31, lg = lane >> 5;
+  // -Delta of the block's rows in the S-result layout (register 4a+e = row 8a+4lg+e) is
+  // the dP accumulator's starting value; LSE*log2e in the same layout.
+  f32x16 nd, lv;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const f32x4 x = *reinterpret_cast<const f32x4 *>(nd_t + qb * 32 + 8 * a + 4 * lg);
+    const f32x4 y = *reinterpret_cast<const f32x4 *>(lse_t + qb * 32 + 8 * a + 4 * lg);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      nd[4 * a + e] = x[e];
+      lv[4 * a + e] = y[e];
+    }
+  }
+  bf16x8 qa[P::KK], da[P::KK];
+#pragma unroll
+  for (int kk = 0; kk < P::KK; ++kk) {
+    qa[kk] = lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg);
+    da[kk] = lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg);
+  }
+  f32x16 s = mfma32(qa[0], kf[0], f32x16{});
+  f32x16 dp = mfma32(da[0], vf[0], nd);
+#pragma unroll
+  for (int kk = 1; kk < P::KK; ++kk) {
+    s = mfma32(qa[kk], kf[kk], s);
+    dp = mfma32(da[kk], vf[kk], dp);
+  }
+  f32x16 ds;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = __builtin_fmaf(s[r], scale_log2, -lv[r]);
+    if (MASK) {
+      const int qr = qbase + 8 * (r >> 2) + 4 * lg + (r & 3);
+      if (krow > qr || qr >= T) x = -INFINITY;
+    }
+    const float p = exp2f_fast(x);
+    s[r] = p;
+    ds[r] = p * dp[r];
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const bf16x8 pb = pack8(s, 8 * m);
+    const bf16x8 dsb = pack8(ds, 8 * m);
+    bf16x8 dot[P::DB], qt[P::DB];
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) {
+      dot[db] = lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane);
+      qt[db] = lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane);
+    }
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) {
+      dvacc[db] = mfma32(dot[db], pb, dvacc[db]);
+      dkacc[db] = mfma32(qt[db], dsb, dkacc[db]);
+    }
+  }
+}
+
+}  // namespace
 
 // ---------------------------------------------------------------- pass 1: Delta + dQ
 template <int D>
@@ -34,8 +175,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
     float scale_log2, float scale) {
-  constexpr int BM = 128, BN = 64;
-  constexpr int KK = D / 16, DB = D / 32, CH = D / 8, LOADS = BN * CH / 256;
+  using P = DqTile<D>;
+  constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
   bf16 *const lds = smem;  // [stage 2][K|V][BN*D]
 
@@ -60,25 +201,6 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
   const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
   const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
 
-  bf16x8 qf[KK], dof[KK];
-  float dpart = 0.f;
-#pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2;
-    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
-    dof[kk] = __builtin_bit_cast(bf16x8, buf_load16(rdo, off));
-    const bf16x8 of = __builtin_bit_cast(bf16x8, buf_load16(ro, off));
-#pragma unroll
-    for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[s]), bf2f(dof[kk][s]), dpart);
-  }
-  const float delta = xhalf_sum(dpart);
-  float lse_t = 0.f;
-  if (qrow < T) {
-    lse_t = LSE[(int64_t)bh * T + qrow] * kLog2e;
-    if (lg == 0) Delta[(int64_t)bh * T + qrow] = delta;
-  }
-
-  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
   u32x4 kreg[LOADS], vreg[LOADS];
   auto load_tile = [&](int j) {
 #pragma unroll
@@ -100,49 +222,47 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
     }
   };
 
+  bf16x8 qf[KK], dof[KK];
+  float dpart = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2;
+    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
+    dof[kk] = __builtin_bit_cast(bf16x8, buf_load16(rdo, off));
+    const bf16x8 of = __builtin_bit_cast(bf16x8, buf_load16(ro, off));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[s]), bf2f(dof[kk][s]), dpart);
+  }
+  const float delta = xhalf_sum(dpart);
+  float lse_t = 0.f;
+  if (qrow < T) {
+    lse_t = LSE[(int64_t)bh * T + qrow] * kLog2e;
+    if (lg == 0) Delta[(int64_t)bh * T + qrow] = delta;
+  }
+  f32x16 ndelta;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ndelta[r] = -delta;
+
+  load_tile(0);
+  store_tile(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no register load is pending in the loop
+  __syncthreads();
+
+  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
+  const int n_full = min((q0 + 1) / BN, T / BN);
+  const int n_vis = min(n_kv, (q0 + 31) / BN + 1);
+
   f32x16 dqacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
   for (int j = 0; j < n_kv; ++j) {
     if (j + 1 < n_kv) load_tile(j + 1);
     const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
-    const int k0 = j * BN;
-    if (k0 <= q0 + 31) {
-      f32x16 s[2], dp[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = f32x16{};
-        dp[kb] = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          s[kb] = mfma32(lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg), qf[kk], s[kb]);
-          dp[kb] = mfma32(lds_read_row8<D>(Vt, kb * 32 + lq, 2 * kk + lg), dof[kk], dp[kb]);
-        }
-      }
-      const bool masked = (k0 + BN - 1 > q0) || (k0 + BN > T);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float p = exp2f_fast(__builtin_fmaf(s[kb][r], scale_log2, -lse_t));
-          if (masked) {
-            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-            if (key > qrow || key >= T) p = 0.f;
-          }
-          s[kb][r] = p * (dp[kb][r] - delta);  // dS^T
-        }
-#pragma unroll
-      for (int m = 0; m < BN / 16; ++m) {
-        const bf16x8 dsb = pack8(s[m >> 1], 8 * (m & 1));
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          dqacc[db] = mfma32(lds_read_trT<D>(Kt, 16 * m, 32 * db, lane), dsb, dqacc[db]);
-      }
-    }
+    if (j < n_full)
+      dq_tile<D, false>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
+    else if (j < n_vis)
+      dq_tile<D, true>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
     if (j + 1 < n_kv) store_tile((j + 1) & 1);
     __syncthreads();
   }
@@ -166,10 +286,9 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
     const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
     int Hq, int Hkv, int T, float scale_log2, float scale) {
-  constexpr int BNK = 128, BMQ = 64;
-  constexpr int KK = D / 16, DB = D / 32, CH = D / 8, LOADS = BMQ * CH / 256;
+  using P = DkvTile<D>;
+  constexpr int BNK = P::BNK, BMQ = P::BMQ, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  // [stage 2][Q|dO][BMQ*D] bf16, then [stage 2][LSE*log2e | Delta][BMQ] fp32
   bf16 *const lds = smem;
   float *const ldsf = reinterpret_cast<float *>(smem + 2 * 2 * BMQ * D);
 
@@ -205,7 +324,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
   const int n_items = G * per_g;
 
   u32x4 qreg[LOADS], doreg[LOADS];
-  float fl = 0.f;  // one LSE*log2e or Delta value for threads < 128
+  float fl = 0.f;  // one LSE*log2e or -Delta value for threads < 128
   auto load_item = [&](int it) {
     const int g = it / per_g, qt = qt_lo + it % per_g;
     const int64_t bhq = (int64_t)b * Hq + hk * G + g;
@@ -221,7 +340,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
     if (tid < 2 * BMQ) {
       const int r = qt * BMQ + (tid & (BMQ - 1));
       fl = 0.f;
-      if (r < T) fl = tid < BMQ ? LSE[bhq * T + r] * kLog2e : Delta[bhq * T + r];
+      if (r < T) fl = tid < BMQ ? LSE[bhq * T + r] * kLog2e : -Delta[bhq * T + r];
     }
   };
   auto store_item = [&](int stage) {
@@ -247,52 +366,24 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
     load_item(0);
     store_item(0);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
   __syncthreads();
   for (int it = 0; it < n_items; ++it) {
     if (it + 1 < n_items) load_item(it + 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-    const float *lse_t = ldsf + stage * 2 * BMQ, *dl = lse_t + BMQ;
+    const float *lse_t = ldsf + stage * 2 * BMQ, *nd_t = lse_t + BMQ;
     const int qt = qt_lo + it % per_g;
 #pragma unroll
     for (int qb = 0; qb < BMQ / 32; ++qb) {
       const int qbase = qt * BMQ + qb * 32;
       if (qbase + 31 < k0w) continue;  // every row of the block precedes every key
-      f32x16 s = f32x16{}, dp = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        s = mfma32(lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg), kf[kk], s);
-        dp = mfma32(lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg), vf[kk], dp);
-      }
-      const bool masked = (qbase < k0w + 31) || (qbase + 31 >= T);
-      f32x16 ds;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int rl = qb * 32 + 8 * a + 4 * lg;  // local row of register 4a
-        const f32x4 lv = *reinterpret_cast<const f32x4 *>(lse_t + rl);
-        const f32x4 dv4 = *reinterpret_cast<const f32x4 *>(dl + rl);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * a + e;
-          float p = exp2f_fast(__builtin_fmaf(s[r], scale_log2, -lv[e]));
-          if (masked) {
-            const int qr = qt * BMQ + rl + e;
-            if (krow > qr || qr >= T) p = 0.f;
-          }
-          s[r] = p;
-          ds[r] = p * (dp[r] - dv4[e]);
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const bf16x8 pb = pack8(s, 8 * m);
-        const bf16x8 dsb = pack8(ds, 8 * m);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          dvacc[db] = mfma32(lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane), pb, dvacc[db]);
-          dkacc[db] = mfma32(lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane), dsb, dkacc[db]);
-        }
-      }
+      if (qbase >= k0w + 31 && qbase + 31 < T)
+        dkdv_block<D, false>(Qt, dOt, lse_t, nd_t, kf, vf, dkacc, dvacc, qb, qbase, krow, T,
+                             scale_log2, lane);
+      else
+        dkdv_block<D, true>(Qt, dOt, lse_t, nd_t, kf, vf, dkacc, dvacc, qb, qbase, krow, T,
+                            scale_log2, lane);
     }
     if (it + 1 < n_items) store_item((it + 1) & 1);
     __syncthreads();
@@ -322,52 +413,57 @@ static hipError_t allow_lds(Kern kern, size_t bytes) {
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+template <int D>
+static hipError_t launch_dq(const void *q, const void *k, const void *v, const void *o,
+                            const void *dout, const float *lse, float *delta, void *dq, int B,
+                            int Hq, int Hkv, int T, float scale, hipStream_t stream) {
+  const int n_tiles = (T + DqTile<D>::BM - 1) / DqTile<D>::BM;
+  const dim3 grid((unsigned)(n_tiles * B * Hq)), block(256);
+  constexpr size_t lds = DqTile<D>::LDS_BYTES;
+  auto kern = fa_bwd_dq_bf16_kernel<D>;
+  if (lds > 65536) {
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+  }
+  kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                     (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
+                                     B, Hq, Hkv, T, scale * kLog2e, scale);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const void *dout,
+                              const float *lse, const float *delta, void *dk, void *dv, int B,
+                              int Hq, int Hkv, int T, float scale, hipStream_t stream) {
+  const int n_ktiles = (T + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
+  const dim3 grid((unsigned)(n_ktiles * B * Hkv)), block(256);
+  constexpr size_t lds = DkvTile<D>::LDS_BYTES;
+  auto kern = fa_bwd_dkdv_bf16_kernel<D>;
+  if (lds > 65536) {
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+  }
+  kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                     (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv, B,
+                                     Hq, Hkv, T, scale * kLog2e, scale);
+  return hipGetLastError();
+}
+
 hipError_t launch_bwd_dq_bf16(const void *q, const void *k, const void *v, const void *o,
                               const void *dout, const float *lse, float *delta, void *dq,
                               int B, int Hq, int Hkv, int T, int D, float scale,
                               hipStream_t stream) {
-  const int n_tiles = (T + 127) / 128;
-  const dim3 grid((unsigned)(n_tiles * B * Hq)), block(256);
-  const float sl2 = scale * kLog2e;
-  const size_t lds = (size_t)2 * 2 * 64 * D * 2;
-  if (D == 64) {
-    auto kern = fa_bwd_dq_bf16_kernel<64>;
-    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
-                                       (const bf16 *)o, (const bf16 *)dout, lse, delta,
-                                       (bf16 *)dq, B, Hq, Hkv, T, sl2, scale);
-  } else {
-    auto kern = fa_bwd_dq_bf16_kernel<128>;
-    hipError_t e = allow_lds(kern, lds);
-    if (e != hipSuccess) return e;
-    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
-                                       (const bf16 *)o, (const bf16 *)dout, lse, delta,
-                                       (bf16 *)dq, B, Hq, Hkv, T, sl2, scale);
-  }
-  return hipGetLastError();
+  return D == 64 ? launch_dq<64>(q, k, v, o, dout, lse, delta, dq, B, Hq, Hkv, T, scale, stream)
+                 : launch_dq<128>(q, k, v, o, dout, lse, delta, dq, B, Hq, Hkv, T, scale, stream);
 }
 
 hipError_t launch_bwd_dkdv_bf16(const void *q, const void *k, const void *v, const void *dout,
                                 const float *lse, const float *delta, void *dk, void *dv,
                                 int B, int Hq, int Hkv, int T, int D, float scale,
                                 hipStream_t stream) {
-  const int n_ktiles = (T + 127) / 128;
-  const dim3 grid((unsigned)(n_ktiles * B * Hkv)), block(256);
-  const float sl2 = scale * kLog2e;
-  const size_t lds = (size_t)2 * 2 * 64 * D * 2 + 2 * 2 * 64 * 4;
-  if (D == 64) {
-    auto kern = fa_bwd_dkdv_bf16_kernel<64>;
-    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
-                                       (const bf16 *)dout, lse, delta, (bf16 *)dk,
-                                       (bf16 *)dv, B, Hq, Hkv, T, sl2, scale);
-  } else {
-    auto kern = fa_bwd_dkdv_bf16_kernel<128>;
-    hipError_t e = allow_lds(kern, lds);
-    if (e != hipSuccess) return e;
-    kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
-                                       (const bf16 *)dout, lse, delta, (bf16 *)dk,
-                                       (bf16 *)dv, B, Hq, Hkv, T, sl2, scale);
-  }
-  return hipGetLastError();
+  return D == 64
+             ? launch_dkdv<64>(q, k, v, dout, lse, delta, dk, dv, B, Hq, Hkv, T, scale, stream)
+             : launch_dkdv<128>(q, k, v, dout, lse, delta, dk, dv, B, Hq, Hkv, T, scale, stream);
 }
 
 }  // namespace ttfa

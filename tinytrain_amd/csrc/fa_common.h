@@ -85,9 +85,22 @@ __device__ __forceinline__ bf16x8 lds_read_trT(const bf16 *tile, int R0, int C0,
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// IEEE maximum (NaN-propagating): lowers to v_maximum3_f32 trees with no per-input
+// canonicalisation, unlike fmaxf (maxnum), which quiets every MFMA result first.
+__device__ __forceinline__ float fmax2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmax2(a, fmax2(b, c)); }
+
+// max over the 16 values of one MFMA result register block
+__device__ __forceinline__ float max16(const f32x16 &v, float init) {
+  float m = fmax3(init, v[0], v[1]);
+#pragma unroll
+  for (int r = 2; r < 16; r += 2) m = fmax3(m, v[r], v[r + 1]);
+  return m;
+}
+
 __device__ __forceinline__ float xhalf_max(float x) {
   auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  return fmax2(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
 __device__ __forceinline__ float xhalf_sum(float x) {

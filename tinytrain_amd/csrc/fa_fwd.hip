@@ -10,30 +10,114 @@
 //
 // Per wave and tile, scores are formed transposed, S^T = K Q^T (32x32x16 MFMAs with K
 // from LDS as the A operand and the wave's Q rows held in registers as the B operand),
-// so every lane owns ONE query row and 16 of the 32 keys of a block: the row max and
-// row sum are in-register reductions plus one v_permlane32_swap.  P^T stays in the
-// result registers and feeds O^T += V^T P^T directly as the B operand; V^T comes from
-// LDS through ds_read_b64_tr_b16, whose row order matches the MFMA result layout, so
-// no register shuffles are needed.  O^T is rescaled per lane (one query per lane).
-// Tiles entirely above the diagonal are never loaded; tiles that cross the diagonal
-// or the ragged end of T are masked; all others take an unmasked path.
-// Softmax runs in the exp2 domain (scale * log2(e) folded into one FMA); the stored
-// LSE is converted back to natural log.
+// so every lane owns ONE query row and 16 of the 32 keys of a block: the row max is an
+// in-register v_max3 tree plus one v_permlane32_swap.  P^T stays in the result
+// registers, is packed to bf16 and feeds O^T += V^T P^T directly as the B operand; V^T
+// comes from LDS through ds_read_b64_tr_b16, whose row order matches the MFMA result
+// layout.  The row sum is accumulated from the fp32 probabilities (a sum of the
+// bf16-rounded values would put up to 2^-9 relative error into LSE for rows that one
+// key dominates, more than the 1e-3 LSE tolerance allows).
+//
+// Softmax runs in the exp2 domain (scale * log2(e) folded into one FMA).  The running
+// max is updated lazily: O and l are rescaled only when some row's tile max exceeds
+// the running max by more than kRescaleSlack (log2 units), so p <= 2^kRescaleSlack and
+// most tiles skip the rescale entirely.  The stored LSE is converted back to natural
+// log.  Tiles entirely above the diagonal are never loaded; only tiles that cross the
+// diagonal or the ragged end of T run the masked body.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
 namespace ttfa {
+
+namespace {
+
+constexpr float kRescaleSlack = 8.0f;
+
+template <int D>
+struct FwdTile {
+  static constexpr int BM = 128, BN = 64;
+  static constexpr int KK = D / 16;            // MFMA k-steps over D
+  static constexpr int DB = D / 32;            // 32-row blocks of O^T
+  static constexpr int CH = D / 8;             // 16-byte chunks per row
+  static constexpr int LOADS = BN * CH / 256;  // 16-byte loads per thread per K (or V) tile
+};
+
+// One 64-key tile for one wave: S^T, online softmax, O^T += V^T P^T.
+template <int D, bool MASK>
+__device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const bf16x8 (&qf)[D / 16],
+                                         f32x16 (&oacc)[D / 32], float &m_t, float &l_part,
+                                         float scale_log2, int k0, int qrow, int T, int lane) {
+  using P = FwdTile<D>;
+  const int lq = lane & 31, lg = lane >> 5;
+
+  // All K operand fragments first, so the LDS reads overlap each other and the MFMAs.
+  bf16x8 kf[2][P::KK];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int kk = 0; kk < P::KK; ++kk) kf[kb][kk] = lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg);
+  f32x16 s[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    s[kb] = mfma32(kf[kb][0], qf[0], f32x16{});
+#pragma unroll
+    for (int kk = 1; kk < P::KK; ++kk) s[kb] = mfma32(kf[kb][kk], qf[kk], s[kb]);
+  }
+  if (MASK) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (key > qrow || key >= T) s[kb][r] = -INFINITY;
+      }
+  }
+  // Row max of this tile (v_max3 tree), then the lazy running-max update.
+  float mx = max16(s[1], max16(s[0], -INFINITY));
+  mx = xhalf_max(mx) * scale_log2;
+  if (__builtin_amdgcn_ballot_w64(mx > m_t + kRescaleSlack)) {  // wave-uniform branch
+    const float m_new = fmax2(m_t, mx);
+    const float alpha = exp2f_fast(m_t - m_new);
+    m_t = m_new;
+    l_part *= alpha;
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) oacc[db] *= alpha;
+  }
+  // P = exp2(S * scale*log2e - m) in fp32 (row sum), packed to bf16 for the PV product.
+  bf16x8 pb[4];
+  float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = exp2f_fast(__builtin_fmaf(s[m >> 1][8 * (m & 1) + e], scale_log2, -m_t));
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      rs0 += p[e];
+      rs1 += p[e + 1];
+    }
+    pb[m] = pack8(f32x16{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]}, 0);
+  }
+  l_part += rs0 + rs1;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    bf16x8 vf[P::DB];
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) vf[db] = lds_read_trT<D>(Vt, 16 * m, 32 * db, lane);
+#pragma unroll
+    for (int db = 0; db < P::DB; ++db) oacc[db] = mfma32(vf[db], pb[m], oacc[db]);
+  }
+}
+
+}  // namespace
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     bf16 *__restrict__ O, float *__restrict__ LSE, int B, int Hq, int Hkv, int T,
     float scale_log2) {
-  constexpr int BM = 128, BN = 64;
-  constexpr int KK = D / 16;           // MFMA k-steps over D
-  constexpr int DB = D / 32;           // 32-row blocks of O^T
-  constexpr int CH = D / 8;            // 16-byte chunks per row
-  constexpr int LOADS = BN * CH / 256; // 16-byte loads per thread per K (or V) tile
+  using P = FwdTile<D>;
+  constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   __shared__ __attribute__((aligned(16))) bf16 lds[2][2][BN * D];  // [stage][K|V]
 
   const int n_tiles = (T + BM - 1) / BM;
@@ -50,20 +134,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
   const int qrow = q0 + lq;
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const bf16 *Qh = Q + (int64_t)bh * T * D;
-  const auto rq = make_rsrc(Qh, head_bytes);
+  const auto rq = make_rsrc(Q + (int64_t)bh * T * D, head_bytes);
   const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
   const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
-
-  // Q^T as B operand: lane (lq, lg) slot s of step kk holds Q[qrow][16kk + 8lg + s].
-  bf16x8 qf[KK];
-#pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    u32x4 raw = buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2);
-    qf[kk] = __builtin_bit_cast(bf16x8, raw);
-  }
-
-  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
 
   u32x4 kreg[LOADS], vreg[LOADS];
   auto load_tile = [&](int j) {
@@ -85,68 +158,38 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
     }
   };
 
+  // Q^T as B operand: lane (lq, lg) slot s of step kk holds Q[qrow][16kk + 8lg + s].
+  bf16x8 qf[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
+  load_tile(0);
+  store_tile(0);
+  // Every load issued so far (Q and the first tile) is complete here, so the loop body
+  // never waits on the Q registers behind the next tile's prefetch.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+
+  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
+  // Tiles [0, n_full) are visible to every row of this wave and lie inside T;
+  // tiles [n_full, n_vis) need the mask; later tiles are skipped by this wave.
+  const int n_full = min((q0 + 1) / BN, T / BN);
+  const int n_vis = min(n_kv, (q0 + 31) / BN + 1);
+
   f32x16 oacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = f32x16{};
   float m_t = -INFINITY;  // running row max, in scale*log2(e) units
   float l_part = 0.f;     // this lane's share of the running row sum
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
   for (int j = 0; j < n_kv; ++j) {
     if (j + 1 < n_kv) load_tile(j + 1);
     const bf16 *Kt = lds[j & 1][0];
     const bf16 *Vt = lds[j & 1][1];
-    const int k0 = j * BN;
-    if (k0 <= q0 + 31) {  // some key of this tile is visible to some row of the wave
-      f32x16 s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-          s[kb] = mfma32(lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg), qf[kk], s[kb]);
-      }
-      if (k0 + BN - 1 > q0 || k0 + BN > T) {  // diagonal or ragged tile
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-            if (key > qrow || key >= T) s[kb][r] = -INFINITY;
-          }
-      }
-      float mx = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-      mx = xhalf_max(mx);
-      const float m_new = fmaxf(m_t, mx * scale_log2);
-      const float alpha = exp2f_fast(m_t - m_new);
-      m_t = m_new;
-      float rs = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2f_fast(__builtin_fmaf(s[kb][r], scale_log2, -m_new));
-          s[kb][r] = p;
-          rs += p;
-        }
-      l_part = l_part * alpha + rs;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-#pragma unroll
-      for (int m = 0; m < BN / 16; ++m) {
-        const bf16x8 pb = pack8(s[m >> 1], 8 * (m & 1));
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          oacc[db] = mfma32(lds_read_trT<D>(Vt, 16 * m, 32 * db, lane), pb, oacc[db]);
-      }
-    }
+    if (j < n_full)
+      fwd_tile<D, false>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
+    else if (j < n_vis)
+      fwd_tile<D, true>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
     if (j + 1 < n_kv) store_tile((j + 1) & 1);
     __syncthreads();
   }
@@ -164,7 +207,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
             pack4(oacc[db][4 * a] * inv, oacc[db][4 * a + 1] * inv, oacc[db][4 * a + 2] * inv,
                   oacc[db][4 * a + 3] * inv);
       }
-    if (lg == 0) LSE[(int64_t)bh * T + qrow] = m_t * kLn2 + __logf(l);
+    if (lg == 0) LSE[(int64_t)bh * T + qrow] = (m_t + __log2f(l)) * kLn2;
   }
 }
 
