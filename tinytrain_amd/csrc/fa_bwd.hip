@@ -4,9 +4,10 @@
 // :208-209) instead of storing it:
 //
 //  1. dQ pass (reference: bwd_preprocess :70-90 fused with bwd_dq_kernel :162-217).
-//     One workgroup = 128 query rows of one (batch, head), 4 waves x 32 rows, longest
-//     rows first.  The prologue computes Delta = rowsum(O * dO) for the workgroup's
-//     own rows from the same registers that hold dO, and writes it to the workspace
+//     A row tile = 128 query rows of one (batch, head), 4 waves x 32 rows; each
+//     workgroup takes a balanced pair of row tiles, the longer first (pair_item).
+//     The prologue computes Delta = rowsum(O * dO) for the tile's own rows from the
+//     same registers that hold dO, and writes it to the workspace
 //     for pass 2 (so there is no separate preprocess launch and dO is read once here).
 //     Per key tile from LDS (64 keys for D=64, 32 for D=128):  S^T = K Q^T and
 //     dP^T - Delta = V dO^T - Delta (the dP accumulator starts at -Delta, a per-lane
@@ -14,8 +15,9 @@
 //     dS^T = P^T (dP^T - Delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
 //     Every lane owns one query row, so LSE and Delta are per-lane scalars.
 //
-//  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  One workgroup = 128 keys of one
-//     (batch, kv head), 4 waves x 32 keys; the wave's K and V rows stay in registers.
+//  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  A key tile = 128 keys of one
+//     (batch, kv head), 4 waves x 32 keys, and each workgroup takes a balanced pair of
+//     key tiles; the wave's K and V rows stay in registers.
 //     The workgroup walks the G query heads of its group and, for each, the 64-row Q
 //     tiles from the diagonal to the end, double-buffered through LDS together with the
 //     tiles' LSE*log2e and -Delta; dK and dV accumulate in registers across the whole
@@ -169,21 +171,18 @@ __device__ __forceinline__ void dkdv_block(const bf16 *Qt, const bf16 *dOt, cons
 }  // namespace
 
 // ---------------------------------------------------------------- pass 1: Delta + dQ
+// Delta and dQ for the 128 query rows of row tile qt of head bh.  Ends with a
+// workgroup barrier, so the caller may reuse the LDS ring right away.
 template <int D>
-__global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
-    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-    const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
-    float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
-    float scale_log2, float scale) {
+__device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
+                                        const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+                                        const bf16 *__restrict__ O, const bf16 *__restrict__ dO,
+                                        const float *__restrict__ LSE, float *__restrict__ Delta,
+                                        bf16 *__restrict__ dQ, int bh, int qt, int Hq, int Hkv,
+                                        int T, float scale_log2, float scale, int work_left,
+                                        int work_max) {
   using P = DqTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  bf16 *const lds = smem;  // [stage 2][K|V][BN*D]
-
-  const int n_tiles = (T + BM - 1) / BM;
-  const TileOrder to = order_tiles(blockIdx.x, n_tiles, B, Hq, Hkv);
-  const int qt = n_tiles - 1 - to.tile;
-  const int bh = to.bh;
   const int G = Hq / Hkv;
   const int b = bh / Hq, h = bh - b * Hq;
   const int64_t kv_head = (int64_t)b * Hkv + h / G;
@@ -257,6 +256,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
   for (int j = 0; j < n_kv; ++j) {
+    prio_by_remaining(work_left - j, work_max);
     if (j + 1 < n_kv) load_tile(j + 1);
     const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
     if (j < n_full)
@@ -267,35 +267,50 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
     __syncthreads();
   }
 
-  if (qrow < T) {
-    bf16 *row = dQ + ((int64_t)bh * T + qrow) * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-        *reinterpret_cast<bf16x4 *>(row + 32 * db + 8 * a + 4 * lg) =
-            pack4(dqacc[db][4 * a] * scale, dqacc[db][4 * a + 1] * scale,
-                  dqacc[db][4 * a + 2] * scale, dqacc[db][4 * a + 3] * scale);
-  }
+  // The loop's last barrier freed the LDS ring: each wave stages its dQ tile in its own
+  // 32*D slice of it for row-contiguous stores.
+  store_rows<D>(dqacc, scale, lds + wave * 32 * D, dQ + (int64_t)bh * T * D, q0, T, lane);
+  __syncthreads();  // the ring is free again for the caller
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
+    float scale_log2, float scale, int paired) {
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];  // [stage 2][K|V][BN*D]
+  using P = DqTile<D>;
+  const int n_tiles = (T + P::BM - 1) / P::BM;
+  const WorkPair w = sched_item(paired, blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
+  // Key tiles a row tile visits is its work; the priority scales by the largest
+  // workgroup's work.
+  const int n_kt = (T + P::BN - 1) / P::BN;
+  auto work = [&](int qt) { return qt < 0 ? 0 : min(n_kt, (qt + 1) * (P::BM / P::BN)); };
+  const int w1 = work(w.first), w2 = work(w.second);
+  const int wmax = paired ? work(n_tiles - 1) + work(0) : work(n_tiles - 1);
+  dq_rows<D>(smem, Q, K, V, O, dO, LSE, Delta, dQ, w.bh, w.first, Hq, Hkv, T, scale_log2, scale,
+             w1 + w2, wmax);
+  if (w.second >= 0)
+    dq_rows<D>(smem, Q, K, V, O, dO, LSE, Delta, dQ, w.bh, w.second, Hq, Hkv, T, scale_log2,
+               scale, w2, wmax);
 }
 
 // ---------------------------------------------------------------- pass 2: dK, dV
+// dK and dV for the 128 keys of key tile kt of kv head bhk (= batch * Hkv + kv head),
+// reduced over the head's query-head group.  Ends with a workgroup barrier, so the
+// caller may reuse the LDS ring right away.
 template <int D>
-__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kernel(
-    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
-    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
-    int Hq, int Hkv, int T, float scale_log2, float scale) {
+__device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
+                                          const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+                                          const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+                                          const float *__restrict__ Delta, bf16 *__restrict__ dK,
+                                          bf16 *__restrict__ dV, int bhk, int kt, int Hq, int Hkv,
+                                          int T, float scale_log2, float scale, int work_left,
+                                          int work_max) {
   using P = DkvTile<D>;
   constexpr int BNK = P::BNK, BMQ = P::BMQ, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  bf16 *const lds = smem;
-  float *const ldsf = reinterpret_cast<float *>(smem + 2 * 2 * BMQ * D);
-
-  const int n_ktiles = (T + BNK - 1) / BNK;
-  const TileOrder to = order_tiles(blockIdx.x, n_ktiles, B, Hkv, Hkv);
-  const int kt = to.tile;  // tile 0 sees the most query rows: longest first
-  const int bhk = to.bh;   // batch * Hkv + kv head
+  float *const ldsf = reinterpret_cast<float *>(lds + 2 * 2 * BMQ * D);
   const int G = Hq / Hkv;
   const int b = bhk / Hkv, hk = bhk - b * Hkv;
 
@@ -369,6 +384,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
   __syncthreads();
   for (int it = 0; it < n_items; ++it) {
+    prio_by_remaining(work_left - it, work_max);
     if (it + 1 < n_items) load_item(it + 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
@@ -389,21 +405,36 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
     __syncthreads();
   }
 
-  if (krow < T) {
-    bf16 *dkrow = dK + kvbase + (int64_t)krow * D;
-    bf16 *dvrow = dV + kvbase + (int64_t)krow * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d = 32 * db + 8 * a + 4 * lg;
-        *reinterpret_cast<bf16x4 *>(dkrow + d) =
-            pack4(dkacc[db][4 * a] * scale, dkacc[db][4 * a + 1] * scale,
-                  dkacc[db][4 * a + 2] * scale, dkacc[db][4 * a + 3] * scale);
-        *reinterpret_cast<bf16x4 *>(dvrow + d) =
-            pack4(dvacc[db][4 * a], dvacc[db][4 * a + 1], dvacc[db][4 * a + 2], dvacc[db][4 * a + 3]);
-      }
-  }
+  // The loop's last barrier freed the LDS ring: each wave stages its dK and dV tiles in
+  // its own two 32*D slices of it for row-contiguous stores.
+  store_rows<D>(dkacc, scale, lds + wave * 64 * D, dK + kvbase, k0w, T, lane);
+  store_rows<D>(dvacc, 1.f, lds + wave * 64 * D + 32 * D, dV + kvbase, k0w, T, lane);
+  __syncthreads();  // the ring is free again for the caller
+}
+
+template <int D>
+__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
+    int Hq, int Hkv, int T, float scale_log2, float scale, int paired) {
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  using P = DkvTile<D>;
+  const int n_ktiles = (T + P::BNK - 1) / P::BNK;
+  // Key tile 0 sees the most query rows, so the longer tile of a pair is the low one.
+  const WorkPair w = sched_item(paired, blockIdx.x, n_ktiles, B, Hkv, 1, true);
+  // Query tiles a key tile visits (times the group's query heads) is its work; the
+  // priority scales by the largest workgroup's work.
+  const int n_qt = (T + P::BMQ - 1) / P::BMQ;
+  const int G = Hq / Hkv;
+  auto work = [&](int kt) { return kt < 0 ? 0 : G * (n_qt - kt * (P::BNK / P::BMQ)); };
+  const int w1 = work(w.first), w2 = work(w.second);
+  const int wmax = paired ? work(0) + work(n_ktiles - 1) : work(0);
+  dkdv_rows<D>(smem, Q, K, V, dO, LSE, Delta, dK, dV, w.bh, w.first, Hq, Hkv, T, scale_log2, scale,
+               w1 + w2, wmax);
+  if (w.second >= 0)
+    dkdv_rows<D>(smem, Q, K, V, dO, LSE, Delta, dK, dV, w.bh, w.second, Hq, Hkv, T, scale_log2,
+                 scale, w2, wmax);
 }
 
 template <typename Kern>
@@ -418,16 +449,17 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
                             const void *dout, const float *lse, float *delta, void *dq, int B,
                             int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   const int n_tiles = (T + DqTile<D>::BM - 1) / DqTile<D>::BM;
-  const dim3 grid((unsigned)(n_tiles * B * Hq)), block(256);
   constexpr size_t lds = DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds(kern, lds);
     if (e != hipSuccess) return e;
   }
+  const bool paired = use_pairs(n_tiles, B, Hq, resident_slots<fa_bwd_dq_bf16_kernel<D>>(256, lds));
+  const dim3 grid((unsigned)sched_items(paired, n_tiles, B, Hq)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
-                                     B, Hq, Hkv, T, scale * kLog2e, scale);
+                                     B, Hq, Hkv, T, scale * kLog2e, scale, (int)paired);
   return hipGetLastError();
 }
 
@@ -436,16 +468,18 @@ static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const
                               const float *lse, const float *delta, void *dk, void *dv, int B,
                               int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   const int n_ktiles = (T + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
-  const dim3 grid((unsigned)(n_ktiles * B * Hkv)), block(256);
   constexpr size_t lds = DkvTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dkdv_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds(kern, lds);
     if (e != hipSuccess) return e;
   }
+  const bool paired =
+      use_pairs(n_ktiles, B, Hkv, resident_slots<fa_bwd_dkdv_bf16_kernel<D>>(256, lds));
+  const dim3 grid((unsigned)sched_items(paired, n_ktiles, B, Hkv)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv, B,
-                                     Hq, Hkv, T, scale * kLog2e, scale);
+                                     Hq, Hkv, T, scale * kLog2e, scale, (int)paired);
   return hipGetLastError();
 }
 

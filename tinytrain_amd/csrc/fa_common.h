@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace ttfa {
 
 typedef __bf16 bf16;
@@ -98,6 +100,35 @@ __device__ __forceinline__ float max16(const f32x16 &v, float init) {
   return m;
 }
 
+// Stores a wave's 32 x D result tile held in MFMA result layout (lane l owns row l%32;
+// register 4a+e of block db holds column 32db + 8a + 4(l/32) + e), times `mul` and
+// rounded to bf16, to rows row0.. of a row-major [T][D] output.  The tile goes through
+// the wave's own LDS scratch (32*D bf16, swizzled like the operand tiles), so every
+// global store instruction writes whole rows: 64 lanes x 16 contiguous bytes, instead of
+// 8-byte pieces of 32 different rows.  Rows at or past T are not written.
+template <int D>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float mul, bf16 *scratch,
+                                           bf16 *out, int row0, int T, int lane) {
+  const int lq = lane & 31, lg = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int col = 32 * db + 8 * a + 4 * lg;
+      const bf16x2 x = __builtin_convertvector((f32x2{acc[db][4 * a] * mul, acc[db][4 * a + 1] * mul}), bf16x2);
+      const bf16x2 y = __builtin_convertvector((f32x2{acc[db][4 * a + 2] * mul, acc[db][4 * a + 3] * mul}), bf16x2);
+      *reinterpret_cast<bf16x4 *>(scratch + lq * D + (swz(lq, col >> 3) << 3) + (col & 7)) =
+          bf16x4{x[0], x[1], y[0], y[1]};
+    }
+  constexpr int CH = D / 8;
+#pragma unroll
+  for (int i = 0; i < 32 * CH / 64; ++i) {
+    const int e = lane + 64 * i, row = e / CH, ch = e % CH;
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(scratch + row * D + (swz(row, ch) << 3));
+    if (row0 + row < T) *reinterpret_cast<u32x4 *>(out + (int64_t)(row0 + row) * D + ch * 8) = v;
+  }
+}
+
 __device__ __forceinline__ float xhalf_max(float x) {
   auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmax2(__uint_as_float(p[0]), __uint_as_float(p[1]));
@@ -127,35 +158,131 @@ __device__ __forceinline__ bf16x4 pack4(float a, float b, float c, float d) {
 
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 
-// Workgroup -> work-item order.  Hardware hands consecutive workgroup ids to the 8
-// XCDs round-robin (id % 8), and each XCD has its own L2.  When the number of
-// (batch, kv-head) groups is a multiple of 8, every group is pinned to one XCD so
-// the Hq/Hkv query heads and all row tiles that read the same K/V share one L2;
-// within an XCD, the longest causal tiles go first.  Otherwise: longest tiles
-// first, heads interleaved.
-struct TileOrder {
-  int tile;  // row-tile index in the "longest first" sense is resolved by the caller
-  int bh;    // batch * Hq + query head
+// Workgroup -> work item.  Causal row tiles carry very different amounts of work (tile t
+// of n sees t+1 key tiles), so every workgroup takes a PAIR of row tiles (n-1-p, p):
+// the pair's total work is the same for every p, and a grid of pairs is one balanced
+// round instead of a long tail behind the diagonal's longest tiles.  The longer tile of
+// the pair runs first.  When n is odd the middle tile forms a pair of its own.
+//
+// Hardware hands consecutive workgroup ids to the 8 XCDs round-robin (id % 8), and each
+// XCD has its own L2.  When the number of (batch, kv-head) groups is a multiple of 8,
+// each group's items (its G query heads x pairs) are placed on one XCD and numbered
+// consecutively there, so the workgroups that read the same K/V run at the same time
+// on the same L2.  Otherwise items are numbered group-major in plain id order.
+struct WorkPair {
+  int bh;      // batch * H + head (H = the caller's head count)
+  int first;   // longer row tile
+  int second;  // shorter row tile, or -1
 };
 
-__device__ __forceinline__ TileOrder order_tiles(int bid, int n_tiles, int B, int Hq, int Hkv) {
-  const int G = Hq / Hkv;
-  const int BHkv = B * Hkv;
-  TileOrder t;
-  if ((BHkv & 7) == 0) {
-    const int x = bid & 7, i = bid >> 3;
-    const int per_rank = (BHkv >> 3) * G;  // work items per tile rank on one XCD
-    t.tile = i / per_rank;
-    const int rem = i - t.tile * per_rank;
-    const int z = (rem / G) * 8 + x;      // batch * Hkv + kv head
-    const int hq = (z % Hkv) * G + rem % G;
-    t.bh = (z / Hkv) * Hq + hq;
+// n_tiles: row tiles per head; H heads per batch, grouped by Hg heads per group
+// (Hg = Hq / Hkv for query-row kernels, 1 for the kv-row kernel); long_first_low: the
+// longest tile is tile n-1 (query rows) when false, tile 0 (key rows) when true.
+__device__ __forceinline__ WorkPair pair_item(int bid, int n_tiles, int B, int H, int Hg,
+                                              bool long_is_low) {
+  const int n_pairs = (n_tiles + 1) / 2;
+  const int per_group = Hg * n_pairs;
+  const int n_groups = B * (H / Hg);
+  int z, i;
+  if ((n_groups & 7) == 0) {
+    const int x = bid & 7, k = bid >> 3;
+    z = (k / per_group) * 8 + x;
+    i = k - (k / per_group) * per_group;
   } else {
-    const int BH = B * Hq;
-    t.tile = bid / BH;
-    t.bh = bid - t.tile * BH;
+    z = bid / per_group;
+    i = bid - z * per_group;
   }
-  return t;
+  const int g = i / n_pairs, p = i - g * n_pairs;
+  WorkPair w;
+  w.bh = z * Hg + g;  // groups are consecutive heads: bh = b*H + hk*Hg + g
+  const int lo = p, hi = n_tiles - 1 - p;
+  w.first = long_is_low ? lo : hi;
+  w.second = lo == hi ? -1 : (long_is_low ? hi : lo);
+  return w;
+}
+
+// Single-tile schedule: one row tile per workgroup, longest tiles first (tile-rank
+// major), with the same XCD grouping as pair_item.  Used when pairs would not fill whole
+// rounds of the resident workgroup slots.
+__device__ __forceinline__ WorkPair single_item(int bid, int n_tiles, int B, int H, int Hg,
+                                                bool long_is_low) {
+  const int n_groups = B * (H / Hg);
+  int rank, z, g;
+  if ((n_groups & 7) == 0) {
+    const int x = bid & 7, k = bid >> 3;
+    const int per_rank = (n_groups >> 3) * Hg;  // items of one tile rank on one XCD
+    rank = k / per_rank;
+    const int rem = k - rank * per_rank;
+    z = (rem / Hg) * 8 + x;
+    g = rem - (rem / Hg) * Hg;
+  } else {
+    const int per_rank = n_groups * Hg;
+    rank = bid / per_rank;
+    const int rem = bid - rank * per_rank;
+    z = rem / Hg;
+    g = rem - z * Hg;
+  }
+  WorkPair w;
+  w.bh = z * Hg + g;
+  w.first = long_is_low ? rank : n_tiles - 1 - rank;
+  w.second = -1;
+  return w;
+}
+
+__device__ __forceinline__ WorkPair sched_item(bool paired, int bid, int n_tiles, int B, int H,
+                                               int Hg, bool long_is_low) {
+  return paired ? pair_item(bid, n_tiles, B, H, Hg, long_is_low)
+                : single_item(bid, n_tiles, B, H, Hg, long_is_low);
+}
+
+// Workgroups a launch needs for n_tiles row tiles per head: paired or single.
+inline int sched_items(bool paired, int n_tiles, int B, int H) {
+  return (paired ? (n_tiles + 1) / 2 : n_tiles) * B * H;
+}
+
+// Workgroups of kernel KERN resident on the whole device at once: CUs x blocks per CU,
+// from the runtime's occupancy calculator, cached per kernel (one value per process: the
+// supported set-up is one MI355X, and every MI355X gives the same value).
+template <auto KERN>
+inline int resident_slots(int block, size_t lds) {
+  static std::atomic<int> cached{0};
+  int v = cached.load(std::memory_order_relaxed);
+  if (v) return v;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(KERN),
+                                                   block, lds) != hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return 1;  // unknown: then pairs are used only when they fill rounds of one slot
+  v = cus * per_cu;
+  cached.store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// Pairs only when they fill whole rounds of the resident slots (or nearly: the last
+// round at least 7/8 full); otherwise single tiles, longest first, keep slots busy.
+inline bool use_pairs(int n_tiles, int B, int H, int slots) {
+  const int items = sched_items(true, n_tiles, B, H);
+  const int rem = items % slots;
+  return n_tiles > 1 && (rem == 0 || 8 * rem >= 7 * slots);
+}
+
+// Wave issue priority from the workgroup's remaining work.  A CU's SIMDs issue from
+// the oldest wave first, so of several equal workgroups sharing a CU the oldest races
+// ahead and the youngest drains alone at the end.  Giving the workgroup with more work
+// left the higher priority (0..3, by quarters of its total) keeps them in step, so the
+// CU stays fully occupied until all of them finish.
+__device__ __forceinline__ void prio_by_remaining(int remaining, int total) {
+  const int lvl = (4 * remaining) / (total > 0 ? total : 1);
+  if (lvl >= 3)
+    __builtin_amdgcn_s_setprio(3);
+  else if (lvl == 2)
+    __builtin_amdgcn_s_setprio(2);
+  else if (lvl == 1)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
 }
 
 }  // namespace ttfa

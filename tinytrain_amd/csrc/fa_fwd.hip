@@ -4,9 +4,11 @@
 // for every query row i of head h, O_i = sum_{j<=i} softmax_j(q_i.k_j * scale) v_j
 // with K/V read from KV head h / G, and LSE_i = m_i + ln(l_i) in natural-log units.
 //
-// Work split: one workgroup = 4 waves = 128 query rows of one (batch, head); each wave
-// owns 32 rows.  K/V stream through LDS in 64-key tiles, double-buffered: the next
-// tile's global loads are in flight while the current tile is consumed.
+// Work split: one workgroup = 4 waves; a row tile is 128 query rows of one (batch, head)
+// and each wave owns 32 of them.  A workgroup processes a pair of row tiles, the longer
+// first, so every workgroup carries the same causal work (pair_item).  K/V stream
+// through LDS in 64-key tiles, double-buffered: the next tile's global loads are in
+// flight while the current tile is consumed.
 //
 // Per wave and tile, scores are formed transposed, S^T = K Q^T (32x32x16 MFMAs with K
 // from LDS as the A operand and the wave's Q rows held in registers as the B operand),
@@ -111,19 +113,17 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
 
 }  // namespace
 
+// All 128 query rows of row tile qt of head bh: online softmax over its key tiles.
+// Ends with a workgroup barrier, so the caller may reuse the LDS ring right away.
 template <int D>
-__global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
-    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-    bf16 *__restrict__ O, float *__restrict__ LSE, int B, int Hq, int Hkv, int T,
-    float scale_log2) {
+__device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
+                                         const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                         const bf16 *__restrict__ V, bf16 *__restrict__ O,
+                                         float *__restrict__ LSE, int bh, int qt, int Hq,
+                                         int Hkv, int T, float scale_log2, int work_left,
+                                         int work_max) {
   using P = FwdTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][BN * D];  // [stage][K|V]
-
-  const int n_tiles = (T + BM - 1) / BM;
-  const TileOrder to = order_tiles(blockIdx.x, n_tiles, B, Hq, Hkv);
-  const int qt = n_tiles - 1 - to.tile;  // longest rows first
-  const int bh = to.bh;
   const int G = Hq / Hkv;
   const int b = bh / Hq, h = bh - b * Hq;
   const int64_t kv_head = (int64_t)b * Hkv + h / G;
@@ -183,6 +183,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
   float l_part = 0.f;     // this lane's share of the running row sum
 
   for (int j = 0; j < n_kv; ++j) {
+    prio_by_remaining(work_left - j, work_max);
     if (j + 1 < n_kv) load_tile(j + 1);
     const bf16 *Kt = lds[j & 1][0];
     const bf16 *Vt = lds[j & 1][1];
@@ -194,36 +195,47 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
     __syncthreads();
   }
 
+  // The loop's last barrier freed the LDS ring: each wave stages its O tile in its own
+  // 32*D slice of it for row-contiguous stores.
   const float l = xhalf_sum(l_part);
-  if (qrow < T) {
-    const float inv = 1.f / l;
-    bf16 *Orow = O + ((int64_t)bh * T + qrow) * D;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d = 32 * db + 8 * a + 4 * lg;
-        *reinterpret_cast<bf16x4 *>(Orow + d) =
-            pack4(oacc[db][4 * a] * inv, oacc[db][4 * a + 1] * inv, oacc[db][4 * a + 2] * inv,
-                  oacc[db][4 * a + 3] * inv);
-      }
-    if (lg == 0) LSE[(int64_t)bh * T + qrow] = (m_t + __log2f(l)) * kLn2;
-  }
+  store_rows<D>(oacc, 1.f / l, &lds[0][0][0] + wave * 32 * D, O + (int64_t)bh * T * D, q0, T, lane);
+  if (qrow < T && lg == 0) LSE[(int64_t)bh * T + qrow] = (m_t + __log2f(l)) * kLn2;
+  __syncthreads();  // the ring is free again for the caller
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    bf16 *__restrict__ O, float *__restrict__ LSE, int B, int Hq, int Hkv, int T,
+    float scale_log2, int paired) {
+  using P = FwdTile<D>;
+  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][P::BN * D];  // [stage][K|V]
+  const int n_tiles = (T + P::BM - 1) / P::BM;
+  const WorkPair w = sched_item(paired, blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
+  // Key tiles a row tile visits is its work; the priority scales by the largest
+  // workgroup's work.
+  const int n_kt = (T + P::BN - 1) / P::BN;
+  auto work = [&](int qt) { return qt < 0 ? 0 : min(n_kt, (qt + 1) * (P::BM / P::BN)); };
+  const int w1 = work(w.first), w2 = work(w.second);
+  const int wmax = paired ? work(n_tiles - 1) + work(0) : work(n_tiles - 1);
+  fwd_rows<D>(lds, Q, K, V, O, LSE, w.bh, w.first, Hq, Hkv, T, scale_log2, w1 + w2, wmax);
+  if (w.second >= 0) fwd_rows<D>(lds, Q, K, V, O, LSE, w.bh, w.second, Hq, Hkv, T, scale_log2, w2, wmax);
 }
 
 hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
                            int B, int Hq, int Hkv, int T, int D, float scale,
                            hipStream_t stream) {
-  const int n_tiles = (T + 127) / 128;
-  const dim3 grid((unsigned)(n_tiles * B * Hq)), block(256);
+  const int n_tiles = (T + FwdTile<64>::BM - 1) / FwdTile<64>::BM;
   const float sl2 = scale * kLog2e;
-  if (D == 64)
-    fa_fwd_bf16_kernel<64><<<grid, block, 0, stream>>>(
-        (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o, lse, B, Hq, Hkv, T, sl2);
-  else
-    fa_fwd_bf16_kernel<128><<<grid, block, 0, stream>>>(
-        (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o, lse, B, Hq, Hkv, T, sl2);
-  return hipGetLastError();
+  auto go = [&](auto kern, int slots) {
+    const bool paired = use_pairs(n_tiles, B, Hq, slots);
+    const dim3 grid((unsigned)sched_items(paired, n_tiles, B, Hq)), block(256);
+    kern<<<grid, block, 0, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o,
+                                     lse, B, Hq, Hkv, T, sl2, (int)paired);
+    return hipGetLastError();
+  };
+  return D == 64 ? go(fa_fwd_bf16_kernel<64>, resident_slots<fa_fwd_bf16_kernel<64>>(256, 0))
+                 : go(fa_fwd_bf16_kernel<128>, resident_slots<fa_fwd_bf16_kernel<128>>(256, 0));
 }
 
 }  // namespace ttfa

@@ -6,7 +6,7 @@
 #include <math.h>
 #include <stdint.h>
 
-#include "../../include/ttfa.h"
+#include "ttfa.h"
 #include "fa_kernels.h"
 
 namespace {
