@@ -20,10 +20,11 @@
 //     key tiles; the wave's K and V rows stay in registers.
 //     The workgroup walks the G query heads of its group and, for each, the 64-row Q
 //     tiles from the diagonal to the end, double-buffered through LDS together with the
-//     tiles' LSE*log2e and -Delta; dK and dV accumulate in registers across the whole
+//     tiles' -LSE/scale and -Delta; dK and dV accumulate in registers across the whole
 //     group, so the group reduction needs no atomics and the result is bitwise
-//     deterministic (reference loop :125-152).  Per wave and 32-row block:  S = Q K^T,
-//     dP - Delta = dO V^T - Delta (accumulator initialised from the staged -Delta),
+//     deterministic (reference loop :125-152).  Per wave and 32-row block:
+//     S - LSE/scale = Q K^T - LSE/scale and dP - Delta = dO V^T - Delta (accumulators
+//     initialised from the staged rows),
 //     P, dS, then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
 //     from LDS.  dK is scaled once at the end (:154).
 //
@@ -52,7 +53,7 @@ struct DkvTile {
   static constexpr int BMQ = 64;                 // query rows per LDS tile
   static constexpr int KK = D / 16, DB = D / 32, CH = D / 8;
   static constexpr int LOADS = BMQ * CH / 256;   // 16-byte loads per thread per Q (or dO) tile
-  // [stage][Q|dO] bf16 tiles, then [stage][LSE*log2e | -Delta] fp32 rows
+  // [stage][Q|dO] bf16 tiles, then [stage][-LSE/scale | -Delta] fp32 rows
   static constexpr int LDS_BYTES = 2 * 2 * BMQ * D * 2 + 2 * 2 * BMQ * 4;
 };
 
@@ -103,67 +104,79 @@ __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf
   }
 }
 
-// One 32-row query block of the dK/dV pass for one wave (its 32 keys).
-template <int D, bool MASK>
-__device__ __forceinline__ void dkdv_block(const bf16 *Qt, const bf16 *dOt, const float *lse_t,
-                                           const float *nd_t, const bf16x8 (&kf)[D / 16],
-                                           const bf16x8 (&vf)[D / 16], f32x16 (&dkacc)[D / 32],
-                                           f32x16 (&dvacc)[D / 32], int qb, int qbase, int krow,
-                                           int T, float scale_log2, int lane) {
+// NB consecutive 32-row query blocks (qb0..) of the dK/dV pass for one wave (its 32 keys).
+// Both accumulator chains of a block start from values staged in LDS in the S-result
+// layout (register 4a+e = row 8a+4lg+e): S from -LSE/scale and dP from -Delta, so
+// P = exp2(S' * scale*log2e) and dS = P (dP - Delta) each take one multiply.  With
+// NB = 2 the blocks' independent MFMA chains and exponentials interleave.
+template <int D, int NB, bool MASK>
+__device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, const float *nls_t,
+                                            const float *nd_t, const bf16x8 (&kf)[D / 16],
+                                            const bf16x8 (&vf)[D / 16], f32x16 (&dkacc)[D / 32],
+                                            f32x16 (&dvacc)[D / 32], int qb0, int qbase0, int krow,
+                                            int T, float scale_log2, int lane) {
   using P = DkvTile<D>;
   const int lq = lane & 31, lg = lane >> 5;
-  // -Delta of the block's rows in the S-result layout (register 4a+e = row 8a+4lg+e) is
-  // the dP accumulator's starting value; LSE*log2e in the same layout.
-  f32x16 nd, lv;
+  f32x16 s[NB], dp[NB];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const f32x4 x = *reinterpret_cast<const f32x4 *>(nd_t + qb * 32 + 8 * a + 4 * lg);
-    const f32x4 y = *reinterpret_cast<const f32x4 *>(lse_t + qb * 32 + 8 * a + 4 * lg);
+  for (int nb = 0; nb < NB; ++nb) {
+    const int qb = qb0 + nb;
+    f32x16 ns, nd;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      nd[4 * a + e] = x[e];
-      lv[4 * a + e] = y[e];
+    for (int a = 0; a < 4; ++a) {
+      const f32x4 x = *reinterpret_cast<const f32x4 *>(nls_t + qb * 32 + 8 * a + 4 * lg);
+      const f32x4 y = *reinterpret_cast<const f32x4 *>(nd_t + qb * 32 + 8 * a + 4 * lg);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ns[4 * a + e] = x[e];
+        nd[4 * a + e] = y[e];
+      }
+    }
+    bf16x8 qa[P::KK], da[P::KK];
+#pragma unroll
+    for (int kk = 0; kk < P::KK; ++kk) {
+      qa[kk] = lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg);
+      da[kk] = lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg);
+    }
+    s[nb] = mfma32(qa[0], kf[0], ns);
+    dp[nb] = mfma32(da[0], vf[0], nd);
+#pragma unroll
+    for (int kk = 1; kk < P::KK; ++kk) {
+      s[nb] = mfma32(qa[kk], kf[kk], s[nb]);
+      dp[nb] = mfma32(da[kk], vf[kk], dp[nb]);
     }
   }
-  bf16x8 qa[P::KK], da[P::KK];
 #pragma unroll
-  for (int kk = 0; kk < P::KK; ++kk) {
-    qa[kk] = lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg);
-    da[kk] = lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg);
-  }
-  f32x16 s = mfma32(qa[0], kf[0], f32x16{});
-  f32x16 dp = mfma32(da[0], vf[0], nd);
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-  for (int kk = 1; kk < P::KK; ++kk) {
-    s = mfma32(qa[kk], kf[kk], s);
-    dp = mfma32(da[kk], vf[kk], dp);
-  }
-  f32x16 ds;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    float x = __builtin_fmaf(s[r], scale_log2, -lv[r]);
-    if (MASK) {
-      const int qr = qbase + 8 * (r >> 2) + 4 * lg + (r & 3);
-      if (krow > qr || qr >= T) x = -INFINITY;
-    }
-    const float p = exp2f_fast(x);
-    s[r] = p;
-    ds[r] = p * dp[r];
-  }
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const bf16x8 pb = pack8(s, 8 * m);
-    const bf16x8 dsb = pack8(ds, 8 * m);
-    bf16x8 dot[P::DB], qt[P::DB];
-#pragma unroll
-    for (int db = 0; db < P::DB; ++db) {
-      dot[db] = lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane);
-      qt[db] = lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane);
+    for (int r = 0; r < 16; ++r) {
+      float x = s[nb][r] * scale_log2;
+      if (MASK) {
+        const int qr = qbase0 + nb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (krow > qr || qr >= T) x = -INFINITY;
+      }
+      const float p = exp2f_fast(x);
+      s[nb][r] = p;
+      dp[nb][r] = p * dp[nb][r];  // dS
     }
 #pragma unroll
-    for (int db = 0; db < P::DB; ++db) {
-      dvacc[db] = mfma32(dot[db], pb, dvacc[db]);
-      dkacc[db] = mfma32(qt[db], dsb, dkacc[db]);
+  for (int nb = 0; nb < NB; ++nb) {
+    const int qb = qb0 + nb;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const bf16x8 pb = pack8(s[nb], 8 * m);
+      const bf16x8 dsb = pack8(dp[nb], 8 * m);
+      bf16x8 dot[P::DB], qt[P::DB];
+#pragma unroll
+      for (int db = 0; db < P::DB; ++db) {
+        dot[db] = lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane);
+        qt[db] = lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane);
+      }
+#pragma unroll
+      for (int db = 0; db < P::DB; ++db) {
+        dvacc[db] = mfma32(dot[db], pb, dvacc[db]);
+        dkacc[db] = mfma32(qt[db], dsb, dkacc[db]);
+      }
     }
   }
 }
@@ -339,7 +352,8 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const int n_items = G * per_g;
 
   u32x4 qreg[LOADS], doreg[LOADS];
-  float fl = 0.f;  // one LSE*log2e or -Delta value for threads < 128
+  const float inv_scale = 1.f / scale;
+  float fl = 0.f;  // one -LSE/scale or -Delta value for threads < 128
   auto load_item = [&](int it) {
     const int g = it / per_g, qt = qt_lo + it % per_g;
     const int64_t bhq = (int64_t)b * Hq + hk * G + g;
@@ -355,7 +369,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
     if (tid < 2 * BMQ) {
       const int r = qt * BMQ + (tid & (BMQ - 1));
       fl = 0.f;
-      if (r < T) fl = tid < BMQ ? LSE[bhq * T + r] * kLog2e : -Delta[bhq * T + r];
+      if (r < T) fl = tid < BMQ ? -LSE[bhq * T + r] * inv_scale : -Delta[bhq * T + r];
     }
   };
   auto store_item = [&](int stage) {
@@ -388,18 +402,25 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
     if (it + 1 < n_items) load_item(it + 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-    const float *lse_t = ldsf + stage * 2 * BMQ, *nd_t = lse_t + BMQ;
+    const float *nls_t = ldsf + stage * 2 * BMQ, *nd_t = nls_t + BMQ;
     const int qt = qt_lo + it % per_g;
+    const int qbase = qt * BMQ;
+    if (qbase >= k0w + 31 && qbase + BMQ - 1 < T) {
+      // every row of the tile sees every key of the wave: both blocks together, unmasked
+      dkdv_blocks<D, BMQ / 32, false>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, 0, qbase, krow,
+                                      T, scale_log2, lane);
+    } else {
 #pragma unroll
-    for (int qb = 0; qb < BMQ / 32; ++qb) {
-      const int qbase = qt * BMQ + qb * 32;
-      if (qbase + 31 < k0w) continue;  // every row of the block precedes every key
-      if (qbase >= k0w + 31 && qbase + 31 < T)
-        dkdv_block<D, false>(Qt, dOt, lse_t, nd_t, kf, vf, dkacc, dvacc, qb, qbase, krow, T,
-                             scale_log2, lane);
-      else
-        dkdv_block<D, true>(Qt, dOt, lse_t, nd_t, kf, vf, dkacc, dvacc, qb, qbase, krow, T,
-                            scale_log2, lane);
+      for (int qb = 0; qb < BMQ / 32; ++qb) {
+        const int qb_row = qbase + qb * 32;
+        if (qb_row + 31 < k0w) continue;  // every row of the block precedes every key
+        if (qb_row >= k0w + 31 && qb_row + 31 < T)
+          dkdv_blocks<D, 1, false>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, qb, qb_row, krow,
+                                   T, scale_log2, lane);
+        else
+          dkdv_blocks<D, 1, true>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, qb, qb_row, krow,
+                                  T, scale_log2, lane);
+      }
     }
     if (it + 1 < n_items) store_item((it + 1) & 1);
     __syncthreads();
