@@ -28,8 +28,9 @@
 //     P, dS, then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
 //     from LDS.  dK is scaled once at the end (:154).
 //
-// Tiles entirely above the diagonal are skipped; only tiles crossing the diagonal or
-// the ragged end of T run the masked body.
+// Both passes fill their LDS tiles with buffer_load ... lds (global -> LDS, 16 bytes per
+// lane, no staging VGPRs).  Tiles entirely above the diagonal are skipped; only tiles
+// crossing the diagonal or the ragged end of T run the masked body.
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -213,24 +214,16 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
   const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
 
-  u32x4 kreg[LOADS], vreg[LOADS];
-  auto load_tile = [&](int j) {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const uint32_t off = (uint32_t)((j * BN + row) * D + ch * 8) * 2;
-      kreg[i] = buf_load16(rk, off);
-      vreg[i] = buf_load16(rv, off);
-    }
-  };
-  auto store_tile = [&](int stage) {
+  // Global -> LDS without registers: lane l of the wave's 1 KB block e0 writes physical
+  // chunk (e0 + l) % CH of row (e0 + l) / CH, which holds logical chunk phys ^ swizzle(row).
+  auto load_tile = [&](int j, int stage) {
     bf16 *Kt = lds + stage * 2 * BN * D, *Vt = Kt + BN * D;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const int off = row * D + (swz(row, ch) << 3);
-      *reinterpret_cast<u32x4 *>(Kt + off) = kreg[i];
-      *reinterpret_cast<u32x4 *>(Vt + off) = vreg[i];
+      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
+      const uint32_t off = (uint32_t)((j * BN + row) * D + swz(row, pc) * 8) * 2;
+      buf_load16_lds(rk, off, Kt + e0 * 8);
+      buf_load16_lds(rv, off, Vt + e0 * 8);
     }
   };
 
@@ -255,8 +248,7 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
 #pragma unroll
   for (int r = 0; r < 16; ++r) ndelta[r] = -delta;
 
-  load_tile(0);
-  store_tile(0);
+  load_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no register load is pending in the loop
   __syncthreads();
 
@@ -270,13 +262,12 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
 
   for (int j = 0; j < n_kv; ++j) {
     prio_by_remaining(work_left - j, work_max);
-    if (j + 1 < n_kv) load_tile(j + 1);
+    if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
     const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
     if (j < n_full)
       dq_tile<D, false>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
       dq_tile<D, true>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
-    if (j + 1 < n_kv) store_tile((j + 1) & 1);
     __syncthreads();
   }
 
@@ -351,20 +342,20 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const int per_g = n_qt - qt_lo;
   const int n_items = G * per_g;
 
-  u32x4 qreg[LOADS], doreg[LOADS];
   const float inv_scale = 1.f / scale;
   float fl = 0.f;  // one -LSE/scale or -Delta value for threads < 128
-  auto load_item = [&](int it) {
+  auto load_item = [&](int it, int stage) {
+    bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
     const int g = it / per_g, qt = qt_lo + it % per_g;
     const int64_t bhq = (int64_t)b * Hq + hk * G + g;
     const auto rq = make_rsrc(Q + bhq * T * D, head_bytes);
     const auto rdo = make_rsrc(dO + bhq * T * D, head_bytes);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + ch * 8) * 2;
-      qreg[i] = buf_load16(rq, off);
-      doreg[i] = buf_load16(rdo, off);
+      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
+      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz(row, pc) * 8) * 2;
+      buf_load16_lds(rq, off, Qt + e0 * 8);
+      buf_load16_lds(rdo, off, dOt + e0 * 8);
     }
     if (tid < 2 * BMQ) {
       const int r = qt * BMQ + (tid & (BMQ - 1));
@@ -372,15 +363,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
       if (r < T) fl = tid < BMQ ? -LSE[bhq * T + r] * inv_scale : -Delta[bhq * T + r];
     }
   };
-  auto store_item = [&](int stage) {
-    bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const int off = row * D + (swz(row, ch) << 3);
-      *reinterpret_cast<u32x4 *>(Qt + off) = qreg[i];
-      *reinterpret_cast<u32x4 *>(dOt + off) = doreg[i];
-    }
+  auto stage_rows = [&](int stage) {
     if (tid < 2 * BMQ) ldsf[stage * 2 * BMQ + tid] = fl;
   };
 
@@ -392,14 +375,14 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
   }
 
   if (n_items > 0) {
-    load_item(0);
-    store_item(0);
+    load_item(0, 0);
+    stage_rows(0);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
   __syncthreads();
   for (int it = 0; it < n_items; ++it) {
     prio_by_remaining(work_left - it, work_max);
-    if (it + 1 < n_items) load_item(it + 1);
+    if (it + 1 < n_items) load_item(it + 1, (it + 1) & 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
     const float *nls_t = ldsf + stage * 2 * BMQ, *nd_t = nls_t + BMQ;
@@ -422,7 +405,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
                                   T, scale_log2, lane);
       }
     }
-    if (it + 1 < n_items) store_item((it + 1) & 1);
+    if (it + 1 < n_items) stage_rows((it + 1) & 1);
     __syncthreads();
   }
 

@@ -50,6 +50,12 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t b
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
 }
 
+// 16 bytes per lane straight from a buffer into LDS: the wave's 64 lanes fill the
+// 1 KB at lds_wave (wave-uniform) in lane order.
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, void *lds_wave) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TTFA_LDS void *)lds_wave, 16, byte_off, 0, 0, 0);
+}
+
 // LDS tiles are row-major [rows][D] bf16, stored in 16-byte chunks whose index is
 // XOR-swizzled by the row: 8 consecutive rows read at one logical chunk (b128 MFMA
 // operand reads) and 4 consecutive rows read at two adjacent chunks (the transposed
@@ -90,7 +96,7 @@ __device__ __forceinline__ bf16x8 lds_read_trT(const bf16 *tile, int R0, int C0,
 // IEEE maximum (NaN-propagating): lowers to v_maximum3_f32 trees with no per-input
 // canonicalisation, unlike fmaxf (maxnum), which quiets every MFMA result first.
 __device__ __forceinline__ float fmax2(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmax2(a, fmax2(b, c)); }
+__device__ __forceinline__ float fmax3(float a, float b, float c) { return fmax2(fmax2(a, b), c); }
 
 // max over the 16 values of one MFMA result register block
 __device__ __forceinline__ float max16(const f32x16 &v, float init) {

@@ -8,7 +8,8 @@
 // and each wave owns 32 of them.  A workgroup processes a pair of row tiles, the longer
 // first, so every workgroup carries the same causal work (pair_item).  K/V stream
 // through LDS in 64-key tiles, double-buffered: the next tile's global loads are in
-// flight while the current tile is consumed.
+// flight while the current tile is consumed.  The loads go from the buffer straight
+// into LDS (buffer_load ... lds, 16 bytes per lane), so no VGPRs stage them.
 //
 // Per wave and tile, scores are formed transposed, S^T = K Q^T (32x32x16 MFMAs with K
 // from LDS as the A operand and the wave's Q rows held in registers as the B operand),
@@ -138,23 +139,17 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
   const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
   const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
 
-  u32x4 kreg[LOADS], vreg[LOADS];
-  auto load_tile = [&](int j) {
+  // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
+  // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
+  // holds logical chunk phys ^ swizzle(row).
+  auto load_tile = [&](int j, int stage) {
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const uint32_t off = (uint32_t)((j * BN + row) * D + ch * 8) * 2;
-      kreg[i] = buf_load16(rk, off);
-      vreg[i] = buf_load16(rv, off);
-    }
-  };
-  auto store_tile = [&](int stage) {
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int e = tid + 256 * i, row = e / CH, ch = e % CH;
-      const int off = row * D + (swz(row, ch) << 3);
-      *reinterpret_cast<u32x4 *>(&lds[stage][0][off]) = kreg[i];
-      *reinterpret_cast<u32x4 *>(&lds[stage][1][off]) = vreg[i];
+      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
+      const int lc = swz(row, pc);
+      const uint32_t off = (uint32_t)((j * BN + row) * D + lc * 8) * 2;
+      buf_load16_lds(rk, off, &lds[stage][0][e0 * 8]);
+      buf_load16_lds(rv, off, &lds[stage][1][e0 * 8]);
     }
   };
 
@@ -163,8 +158,7 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
     qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
-  load_tile(0);
-  store_tile(0);
+  load_tile(0, 0);
   // Every load issued so far (Q and the first tile) is complete here, so the loop body
   // never waits on the Q registers behind the next tile's prefetch.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -184,14 +178,13 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
 
   for (int j = 0; j < n_kv; ++j) {
     prio_by_remaining(work_left - j, work_max);
-    if (j + 1 < n_kv) load_tile(j + 1);
+    if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
     const bf16 *Kt = lds[j & 1][0];
     const bf16 *Vt = lds[j & 1][1];
     if (j < n_full)
       fwd_tile<D, false>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
       fwd_tile<D, true>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
-    if (j + 1 < n_kv) store_tile((j + 1) & 1);
     __syncthreads();
   }
 
