@@ -260,8 +260,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
+  PrioByRemaining prio(work_max);
   for (int j = 0; j < n_kv; ++j) {
-    prio_by_remaining(work_left - j, work_max);
+    prio.update(work_left - j);
     if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
     const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
     if (j < n_full)
@@ -344,15 +345,25 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
 
   const float inv_scale = 1.f / scale;
   float fl = 0.f;  // one -LSE/scale or -Delta value for threads < 128
-  auto load_item = [&](int it, int stage) {
+  // Items run over the group's query heads g, and for each over the query tiles
+  // qt_lo..n_qt-1; (ld_g, ld_qt) is the next item to load.
+  int ld_g = 0, ld_qt = qt_lo;
+  // The load addresses use a scalar copy of the wave index (LDS destinations in SGPRs);
+  // the compute keeps the vector one, which here gives the better register allocation.
+  const int wave_u = wave_id();
+  auto load_item = [&](int stage) {
     bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-    const int g = it / per_g, qt = qt_lo + it % per_g;
+    const int g = ld_g, qt = ld_qt;
+    if (++ld_qt == n_qt) {
+      ld_qt = qt_lo;
+      ++ld_g;
+    }
     const int64_t bhq = (int64_t)b * Hq + hk * G + g;
     const auto rq = make_rsrc(Q + bhq * T * D, head_bytes);
     const auto rdo = make_rsrc(dO + bhq * T * D, head_bytes);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
+      const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
       const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz(row, pc) * 8) * 2;
       buf_load16_lds(rq, off, Qt + e0 * 8);
       buf_load16_lds(rdo, off, dOt + e0 * 8);
@@ -375,19 +386,21 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
   }
 
   if (n_items > 0) {
-    load_item(0, 0);
+    load_item(0);
     stage_rows(0);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
   __syncthreads();
+  PrioByRemaining prio(work_max);
+  int qt = qt_lo;  // query tile of the current item
   for (int it = 0; it < n_items; ++it) {
-    prio_by_remaining(work_left - it, work_max);
-    if (it + 1 < n_items) load_item(it + 1, (it + 1) & 1);
+    prio.update(work_left - it);
+    if (it + 1 < n_items) load_item((it + 1) & 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
     const float *nls_t = ldsf + stage * 2 * BMQ, *nd_t = nls_t + BMQ;
-    const int qt = qt_lo + it % per_g;
     const int qbase = qt * BMQ;
+    if (++qt == n_qt) qt = qt_lo;
     if (qbase >= k0w + 31 && qbase + BMQ - 1 < T) {
       // every row of the tile sees every key of the wave: both blocks together, unmasked
       dkdv_blocks<D, BMQ / 32, false>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, 0, qbase, krow,

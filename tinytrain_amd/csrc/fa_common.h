@@ -56,6 +56,11 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TTFA_LDS void *)lds_wave, 16, byte_off, 0, 0, 0);
 }
 
+// Index of the calling wave in its workgroup as a wave-uniform (scalar) value, so LDS
+// addresses derived from it stay in SGPRs (M0 of the LDS-direct loads needs no
+// v_readfirstlane per load).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // LDS tiles are row-major [rows][D] bf16, stored in 16-byte chunks whose index is
 // XOR-swizzled by the row: 8 consecutive rows read at one logical chunk (b128 MFMA
 // operand reads) and 4 consecutive rows read at two adjacent chunks (the transposed
@@ -279,16 +284,25 @@ inline bool use_pairs(int n_tiles, int B, int H, int slots) {
 // ahead and the youngest drains alone at the end.  Giving the workgroup with more work
 // left the higher priority (0..3, by quarters of its total) keeps them in step, so the
 // CU stays fully occupied until all of them finish.
-__device__ __forceinline__ void prio_by_remaining(int remaining, int total) {
-  const int lvl = (4 * remaining) / (total > 0 ? total : 1);
-  if (lvl >= 3)
-    __builtin_amdgcn_s_setprio(3);
-  else if (lvl == 2)
-    __builtin_amdgcn_s_setprio(2);
-  else if (lvl == 1)
-    __builtin_amdgcn_s_setprio(1);
-  else
-    __builtin_amdgcn_s_setprio(0);
-}
+struct PrioByRemaining {
+  int total, lvl = -1;
+  __device__ explicit PrioByRemaining(int total_) : total(total_ > 0 ? total_ : 1) {}
+  // remaining >= total * k/4 for k = 1, 2, 3 gives level k; s_setprio runs only when the
+  // level changes (its operand is an immediate, hence the branches).
+  __device__ __forceinline__ void update(int remaining) {
+    const int r4 = 4 * remaining;
+    const int l = (r4 >= total) + (r4 >= 2 * total) + (r4 >= 3 * total);
+    if (l == lvl) return;
+    lvl = l;
+    if (l == 3)
+      __builtin_amdgcn_s_setprio(3);
+    else if (l == 2)
+      __builtin_amdgcn_s_setprio(2);
+    else if (l == 1)
+      __builtin_amdgcn_s_setprio(1);
+    else
+      __builtin_amdgcn_s_setprio(0);
+  }
+};
 
 }  // namespace ttfa

@@ -176,8 +176,9 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
   float m_t = -INFINITY;  // running row max, in scale*log2(e) units
   float l_part = 0.f;     // this lane's share of the running row sum
 
+  PrioByRemaining prio(work_max);
   for (int j = 0; j < n_kv; ++j) {
-    prio_by_remaining(work_left - j, work_max);
+    prio.update(work_left - j);
     if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
     const bf16 *Kt = lds[j & 1][0];
     const bf16 *Vt = lds[j & 1][1];
