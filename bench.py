@@ -70,6 +70,16 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
         return time.perf_counter() - t0
 
     run(1)  # warmup
+    backend = "unknown"
+    try:  # which SDPA kernel the CPU build dispatches to (profiler op names)
+        from torch.profiler import ProfilerActivity, profile
+        with profile(activities=[ProfilerActivity.CPU]) as prof:
+            run(1)
+        names = {e.key for e in prof.key_averages()}
+        hits = sorted(n for n in names if "scaled_dot_product" in n or "_flash_attention" in n)
+        backend = ", ".join(hits) if hits else "math (no fused SDPA op)"
+    except Exception as exc:  # profiler unavailable: report, do not fail the baseline
+        backend = f"unknown ({type(exc).__name__})"
     t1 = run(1)
     b = max(1, min(cfg.B, int(1.0 / max(t1, 1e-6))))
     times, spent = [], 0.0
@@ -91,8 +101,32 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
                    f"median of {len(times)} runs ({spent:.1f} s of CPU work)"),
         "seconds_per_sample": round(med, 4),
         "cpu_model": _cpu_model(),
+        "logical_cpus_visible": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count(),
         "torch_threads": torch.get_num_threads(),
+        "sdpa_cpu_ops": backend,
     }
+
+
+def _gemm_reference(dev, n: int = 8192, steps: int = 30) -> dict:
+    """Measured bf16 GEMM throughput (torch.matmul -> hipBLASLt, fp32 accumulate) on an
+    n x n x n problem: the practical matrix-core ceiling the attention numbers are also
+    compared against."""
+    import torch
+
+    a = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=dev, dtype=torch.bfloat16)
+    for _ in range(5):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record()
+        torch.matmul(a, b)
+        e1.record()
+    torch.cuda.synchronize()
+    ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+    return {"shape": [n, n, n], "library": "torch.matmul (hipBLASLt), bf16 in, fp32 accumulate",
+            "median_ms": round(ms, 4), "tflops": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)}
 
 
 TRAFFIC_DIR = ROOT / "profiles"
@@ -105,11 +139,18 @@ def _traffic_file(config: str) -> Path:
 def _pmc_pass(counter: str, cmd: list, out_dir: Path) -> dict:
     """One ``rocprofv3 --pmc <counter>`` pass over ``cmd`` (a child process); returns
     {kernel symbol: mean counter value per dispatch (KiB)}."""
+    return {k: v[counter] for k, v in _pmc_multi([counter], cmd, out_dir).items() if counter in v}
+
+
+def _pmc_multi(counters: list, cmd: list, out_dir: Path) -> dict:
+    """One ``rocprofv3 --pmc c1 c2 ...`` pass over ``cmd`` (a child process); returns
+    {kernel name: {counter: mean value per dispatch}}.  The counters must fit one pass
+    (at most 8 SQ, 4 TCC, 2 GRBM counters)."""
     import csv
     import subprocess
 
     out_dir.mkdir(parents=True, exist_ok=True)
-    full = ["rocprofv3", "--pmc", counter, "-d", str(out_dir), "-o", "run",
+    full = ["rocprofv3", "--pmc", *counters, "-d", str(out_dir), "-o", "run",
             "--output-format", "csv", "--", sys.executable, *cmd]
     print("[traffic] " + " ".join(full), file=sys.stderr, flush=True)
     with open(out_dir / "rocprofv3.log", "w") as log:
@@ -118,12 +159,82 @@ def _pmc_pass(counter: str, cmd: list, out_dir: Path) -> dict:
     sums: dict = {}
     for path in out_dir.rglob("*counter_collection.csv"):
         for row in csv.DictReader(open(path)):
-            if row["Counter_Name"] != counter:
+            if row["Counter_Name"] not in counters:
                 continue
-            name = row["Kernel_Name"]
-            tot, n = sums.get(name, (0.0, 0))
-            sums[name] = (tot + float(row["Counter_Value"]), n + 1)
-    return {k: tot / n for k, (tot, n) in sums.items()}
+            key = (row["Kernel_Name"], row["Counter_Name"])
+            tot, n = sums.get(key, (0.0, 0))
+            sums[key] = (tot + float(row["Counter_Value"]), n + 1)
+    res: dict = {}
+    for (name, ctr), (tot, n) in sums.items():
+        res.setdefault(name, {})[ctr] = tot / n
+    return res
+
+
+# Two passes of SQ counters (8 SQ + 1 GRBM each): matrix-core and vector-ALU activity,
+# LDS bank conflicts.
+SQ_PASSES = (
+    ("SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU",
+     "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_ACTIVE_INST_VALU", "GRBM_GUI_ACTIVE"),
+    ("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_LDS", "SQ_WAIT_INST_ANY",
+     "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_ANY", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_INSTS_SALU",
+     "GRBM_GUI_ACTIVE"),
+)
+
+
+def _measure_sq(config: str, out: Path) -> int:
+    """MFMA-busy, VALU, co-execution and LDS bank-conflict counters per attention kernel
+    on ``config`` (two rocprofv3 --pmc passes), summarised per kernel."""
+    me = str(ROOT / "bench.py")
+    work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
+            "--no-traffic", "--no-extras"]
+    tmp = Path("/tmp") / f"ttfa_sq_{os.getpid()}"
+    merged: dict = {}
+    for i, ctrs in enumerate(SQ_PASSES):
+        for name, vals in _pmc_multi(list(ctrs), [me, *work], tmp / f"pass{i}").items():
+            if "ttfa::" not in name:
+                continue
+            sym = name.split("ttfa::", 1)[1].split("(", 1)[0]
+            d = merged.setdefault(sym, {})
+            for c, v in vals.items():
+                d[c if c != "GRBM_GUI_ACTIVE" else f"GRBM_GUI_ACTIVE_{i}"] = v
+    simds, xcds = 1024, 8  # MI355X: 256 CUs x 4 SIMDs; GRBM_GUI_ACTIVE sums the 8 XCDs
+    rows, summary = [], {}
+    for sym, c in sorted(merged.items()):
+        gui = c.get("GRBM_GUI_ACTIVE_0", float("nan")) / xcds
+        waves = max(c.get("SQ_WAVES", 1.0), 1.0)
+        r = {
+            "mfma_busy": c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * simds),
+            "valu_mfma_coexec": c["SQ_VALU_MFMA_COEXEC_CYCLES"] / (gui * simds),
+            "lds_bank_conflict_per_active": c["SQ_LDS_BANK_CONFLICT"] / max(c["SQ_LDS_IDX_ACTIVE"], 1.0),
+            "valu_insts_per_wave": c["SQ_INSTS_VALU"] / waves,
+            "mfma_insts_per_wave": c["SQ_INSTS_MFMA"] / waves,
+            "lds_insts_per_wave": c["SQ_INSTS_LDS"] / waves,
+            "salu_insts_per_wave": c["SQ_INSTS_SALU"] / waves,
+            "wait_inst_any_frac": c["SQ_WAIT_INST_ANY"] / max(c["SQ_WAVE_CYCLES"], 1.0),
+            "waves": waves,
+        }
+        summary[sym] = {k: round(v, 4) for k, v in r.items()}
+        rows.append(f"{sym:<32}{r['mfma_busy']:>9.3f}{r['valu_mfma_coexec']:>9.3f}"
+                    f"{r['lds_bank_conflict_per_active']:>9.3f}{r['valu_insts_per_wave']:>9.0f}"
+                    f"{r['mfma_insts_per_wave']:>7.0f}{r['lds_insts_per_wave']:>7.0f}"
+                    f"{r['salu_insts_per_wave']:>7.0f}{r['wait_inst_any_frac']:>8.3f}")
+    lines = [
+        f"# SQ activity per attention kernel, workload {config} (rocprofv3 --pmc, two passes)",
+        "# command: python bench.py --measure-sq --config " + config,
+        "# passes:  rocprofv3 --pmc " + " ".join(SQ_PASSES[0]) + " -- python bench.py " + " ".join(work),
+        "#          rocprofv3 --pmc " + " ".join(SQ_PASSES[1]) + " -- python bench.py " + " ".join(work),
+        "# mfma = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE/8 x 1024 SIMDs): matrix-core busy share",
+        "# coex = SQ_VALU_MFMA_COEXEC_CYCLES on the same base: cycles a VALU op issued under a busy MFMA",
+        "# bank = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE: LDS cycles lost to bank conflicts per active cycle",
+        "# per-wave instruction counts; wait = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES",
+        f"{'kernel':<32}{'mfma':>9}{'coex':>9}{'bank':>9}{'VALU/w':>9}{'MFMA':>7}{'LDS':>7}{'SALU':>7}{'wait':>8}",
+        *rows,
+        "JSON " + json.dumps({"config": config, "kernels": summary}),
+    ]
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines), flush=True)
+    return 0
 
 
 def _measure_traffic(config: str, out: Path) -> int:
@@ -131,7 +242,7 @@ def _measure_traffic(config: str, out: Path) -> int:
     scaled by what the same counters read for a plain 256 MB device copy."""
     me = str(ROOT / "bench.py")
     work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
-            "--no-traffic"]
+            "--no-traffic", "--no-extras"]
     copy_mb = 256.0
     copy = ["--copy-probe-mb", str(copy_mb), "--steps", "10"]
     tmp = Path("/tmp") / f"ttfa_traffic_{os.getpid()}"
@@ -228,7 +339,11 @@ def main() -> int:
                          "plain copy, and write the per-kernel HBM traffic summary")
     ap.add_argument("--traffic-out", default="",
                     help="where --measure-traffic writes (default profiles/hbm_traffic_<cfg>.txt)")
+    ap.add_argument("--measure-sq", action="store_true",
+                    help="run two rocprofv3 SQ-counter passes over --config (MFMA busy, VALU, "
+                         "LDS bank conflicts) and write profiles/sq_counters_<cfg>.txt")
     ap.add_argument("--no-traffic", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--no-extras", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -240,6 +355,8 @@ def main() -> int:
     if args.measure_traffic:  # parent never touches the GPU; the passes are children
         out = Path(args.traffic_out) if args.traffic_out else _traffic_file(args.config)
         return _measure_traffic(args.config, out)
+    if args.measure_sq:
+        return _measure_sq(args.config, TRAFFIC_DIR / f"sq_counters_{args.config}.txt")
 
     import torch
 
@@ -312,12 +429,29 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / K
 
-    kms = {"fwd": [], "bwd_dq": [], "bwd_dkdv": []}
-    for ev in evs:
-        kms["fwd"].append(ev[0].elapsed_time(ev[1]))
-        kms["bwd_dq"].append(ev[1].elapsed_time(ev[2]))
-        kms["bwd_dkdv"].append(ev[2].elapsed_time(ev[3]))
+    def per_kernel(evlist):
+        kms = {"fwd": [], "bwd_dq": [], "bwd_dkdv": []}
+        for ev in evlist:
+            kms["fwd"].append(ev[0].elapsed_time(ev[1]))
+            kms["bwd_dq"].append(ev[1].elapsed_time(ev[2]))
+            kms["bwd_dkdv"].append(ev[2].elapsed_time(ev[3]))
+        return kms
+
+    kms = per_kernel(evs)
     avg = {n: sum(x) / len(x) for n, x in kms.items()}
+    med = {n: statistics.median(x) for n, x in kms.items()}
+
+    # Hot-cache pass (outside the timed region above): the same input set every step, so
+    # K/V and Q stay in the Infinity Cache; reported separately.
+    Kh = 0 if args.no_extras else min(K, 50)
+    evh = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(Kh)]
+    for i in range(5 if Kh else 0):
+        launch(sets[0])
+    for i in range(Kh):
+        launch(sets[0], evh[i])
+    torch.cuda.synchronize()
+    hot = {n: statistics.median(x) for n, x in per_kernel(evh).items()} if Kh else None
+    gemm = _gemm_reference(dev) if cfg.dtype == torch.bfloat16 and not args.no_extras else None
 
     fwd_f = cfg.fwd_flop()
     peak = PEAK_BF16_TFLOPS if cfg.dtype == torch.bfloat16 else PEAK_F32_TFLOPS
@@ -364,6 +498,15 @@ def main() -> int:
                     "frac": round(bwd_tflops / peak, 4)},
             "bwd_dq_ms": round(avg["bwd_dq"], 5),
             "bwd_dkdv_ms": round(avg["bwd_dkdv"], 5),
+            "median_ms": {n: round(x, 5) for n, x in med.items()},
+        },
+        "hot_cache": None if hot is None else {
+            "note": "same input set every step (working set resident in the 256 MB Infinity "
+                    "Cache); the headline value above rotates sets to defeat it",
+            "median_ms": {n: round(x, 5) for n, x in hot.items()},
+            "fwd_tflops": round(fwd_f / (hot["fwd"] * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(2.5 * fwd_f / ((hot["bwd_dq"] + hot["bwd_dkdv"]) * 1e-3) / 1e12, 2),
+            "fwd_bwd_tflops": round(3.5 * fwd_f / (sum(hot.values()) * 1e-3) / 1e12, 2),
         },
         "roofline": {
             "bound": "mfma",
@@ -379,6 +522,11 @@ def main() -> int:
         },
         "wall_s_timed": round(wall, 4),
     }
+    if gemm is not None:
+        gemm["step_frac_of_gemm"] = round(step_tflops / gemm["tflops"], 4)
+        gemm["fwd_frac_of_gemm"] = round(fwd_tflops / gemm["tflops"], 4)
+        gemm["bwd_frac_of_gemm"] = round(bwd_tflops / gemm["tflops"], 4)
+        line["gemm_reference"] = gemm
     if args.cpu_budget > 0:
         line["cpu_baseline"] = _cpu_baseline(cfg, args.cpu_budget)
     print(json.dumps(line), flush=True)

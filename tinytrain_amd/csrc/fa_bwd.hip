@@ -221,7 +221,7 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
-      const uint32_t off = (uint32_t)((j * BN + row) * D + swz(row, pc) * 8) * 2;
+      const uint32_t off = (uint32_t)((j * BN + row) * D + swz<D>(row, pc) * 8) * 2;
       buf_load16_lds(rk, off, Kt + e0 * 8);
       buf_load16_lds(rv, off, Vt + e0 * 8);
     }
@@ -364,7 +364,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
-      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz(row, pc) * 8) * 2;
+      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz<D>(row, pc) * 8) * 2;
       buf_load16_lds(rq, off, Qt + e0 * 8);
       buf_load16_lds(rdo, off, dOt + e0 * 8);
     }

@@ -62,21 +62,43 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // LDS tiles are row-major [rows][D] bf16, stored in 16-byte chunks whose index is
-// XOR-swizzled by the row: 8 consecutive rows read at one logical chunk (b128 MFMA
-// operand reads) and 4 consecutive rows read at two adjacent chunks (the transposed
-// b64 reads) both land on distinct 16-byte bank groups.
+// XOR-swizzled by the row.  gfx950's LDS serves 256 bytes (64 banks) per clock: a
+// ds_read_b128 in four groups of 16 consecutive lanes, a ds_read_b64_tr_b16 in two
+// groups of 32; a group runs at full rate when its 16-byte pieces fall on distinct
+// 16-byte bank groups (address bits 4..7).  The access shapes are
+//  * transposed operand reads: rows 4k..4k+3 x chunks 4m..4m+3, and the same 8 rows
+//    further down (lds_read_trT), and
+//  * row operand reads: 16 consecutive rows at one logical chunk (lds_read_row8).
+// The swizzle depends on row bits 0-2 only, so the second half of a transposed read
+// (8 rows down) has the same XOR and its address is the first one plus an immediate;
+// a swizzle that also separates 16 consecutive rows needs row bit 3, and the extra
+// per-lane addresses it costs (VGPRs and VALU in every tile) outweighed the faster row
+// reads in measurements of all three kernels.
+//  D = 64 (128-byte rows, row bit 0 picks the half of a 256-byte window): row bit 1 ->
+//    chunk bit 2, row bit 0 -> bit 1, row bit 2 -> bit 0; rows 4k and 4k+2 (4k+1, 4k+3)
+//    get disjoint chunk groups, so transposed reads are conflict-free; row reads are
+//    2-way.
+//  D = 128 (256-byte rows): row bits 0-1 -> chunk bits 2-3, row bit 2 -> bit 0; the
+//    4 rows of a transposed read get 4 disjoint chunk groups (conflict-free); row reads
+//    are 2-way.
+// Measured read rates of these shapes on MI355X (B/clk/CU at 2.4 GHz, 4 waves/SIMD;
+// linear b128 reads: 213): transposed D=64 188, D=128 190 (121 with row bits 0-1 ->
+// chunk bits 1-2, the D=64 mapping); row reads 122-124 (2-way), 219-221 with a swizzle
+// that uses row bit 3.
+template <int D>
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ (((row & 3) << 1) | ((row >> 2) & 1));
+  if constexpr (D == 128) return chunk ^ (((row & 3) << 2) | ((row >> 2) & 1));
+  else return chunk ^ (((row & 3) << 1) | ((row >> 2) & 1));
 }
 
 template <int D>
 __device__ __forceinline__ int lds_off(int row, int col) {  // element offset of (row, col)
-  return row * D + (swz(row, col >> 3) << 3) + (col & 7);
+  return row * D + (swz<D>(row, col >> 3) << 3) + (col & 7);
 }
 
 template <int D>
 __device__ __forceinline__ bf16x8 lds_read_row8(const bf16 *tile, int row, int chunk) {
-  return *reinterpret_cast<const bf16x8 *>(tile + row * D + (swz(row, chunk) << 3));
+  return *reinterpret_cast<const bf16x8 *>(tile + row * D + (swz<D>(row, chunk) << 3));
 }
 
 __device__ __forceinline__ bf16x4 lds_read_tr(const bf16 *p) {
@@ -128,14 +150,14 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float mu
       const int col = 32 * db + 8 * a + 4 * lg;
       const bf16x2 x = __builtin_convertvector((f32x2{acc[db][4 * a] * mul, acc[db][4 * a + 1] * mul}), bf16x2);
       const bf16x2 y = __builtin_convertvector((f32x2{acc[db][4 * a + 2] * mul, acc[db][4 * a + 3] * mul}), bf16x2);
-      *reinterpret_cast<bf16x4 *>(scratch + lq * D + (swz(lq, col >> 3) << 3) + (col & 7)) =
+      *reinterpret_cast<bf16x4 *>(scratch + lq * D + (swz<D>(lq, col >> 3) << 3) + (col & 7)) =
           bf16x4{x[0], x[1], y[0], y[1]};
     }
   constexpr int CH = D / 8;
 #pragma unroll
   for (int i = 0; i < 32 * CH / 64; ++i) {
     const int e = lane + 64 * i, row = e / CH, ch = e % CH;
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(scratch + row * D + (swz(row, ch) << 3));
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(scratch + row * D + (swz<D>(row, ch) << 3));
     if (row0 + row < T) *reinterpret_cast<u32x4 *>(out + (int64_t)(row0 + row) * D + ch * 8) = v;
   }
 }

@@ -146,7 +146,7 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
-      const int lc = swz(row, pc);
+      const int lc = swz<D>(row, pc);
       const uint32_t off = (uint32_t)((j * BN + row) * D + lc * 8) * 2;
       buf_load16_lds(rk, off, &lds[stage][0][e0 * 8]);
       buf_load16_lds(rv, off, &lds[stage][1][e0 * 8]);
