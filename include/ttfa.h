@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TTFA_ABI_VERSION 1
+#define TTFA_ABI_VERSION 2
 
 enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
 
@@ -47,6 +47,7 @@ enum ttfa_status {
   TTFA_E_ALIGN = -5,       /* a pointer is not 16-byte aligned                   */
   TTFA_E_DTYPE = -6,       /* dtype is not a ttfa_dtype                          */
   TTFA_E_SCALE = -7,       /* scale is not finite and positive                   */
+  TTFA_E_EPS = -8,         /* eps is not in [0, 1)                               */
 };
 
 /* Library ABI version (TTFA_ABI_VERSION of the build). No reference counterpart. */
@@ -98,6 +99,51 @@ int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
                   const float *lse, const float *delta_ws, void *dk, void *dv,
                   int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
                   void *hip_stream);
+
+/*
+ * Fused attention prologue (bf16 only): q/k RMSNorm + rotate-half RoPE + the layout
+ * change from the projections' [B, T, H, D] to the attention's [B, H, T, D].
+ * Replaces model.py:83-93 of the reference (q_norm / k_norm, RMSNorm :24-35, the
+ * transposes, apply_rope :48-56 with cos/sin rounded to bf16, and the .contiguous()
+ * copies before the attention call); no kernel of the reference does this.
+ *
+ *   q_raw            : [B, T, Hq,  D] bf16 contiguous (q_proj output viewed per head)
+ *   k_raw, v_raw     : [B, T, Hkv, D] bf16 contiguous
+ *   q_norm_w, k_norm_w : [D] fp32 RMSNorm weights
+ *   cos, sin         : [T, D] bf16, rows 0..T-1 of the RoPE tables (the reference's
+ *                      fp32 tables rounded to bf16, as apply_rope does)
+ *   q                : [B, Hq,  T, D] bf16 out;  k, v : [B, Hkv, T, D] bf16 out
+ *   rstd_q, rstd_k   : [B, T, Hq] / [B, T, Hkv] fp32 out, 1/sqrt(mean(x^2)+eps) per
+ *                      row (saved for the backward)
+ * Supported: D in {64, 128}, B, T >= 1, Hq % Hkv == 0, eps in [0, 1), every pointer
+ * non-null and 16-byte aligned.  Same status codes as above.
+ */
+int ttfa_qk_prologue_fwd(const void *q_raw, const void *k_raw, const void *v_raw,
+                         const float *q_norm_w, const float *k_norm_w, const void *cos,
+                         const void *sin, void *q, void *k, void *v, float *rstd_q,
+                         float *rstd_k, int B, int T, int Hq, int Hkv, int D, float eps,
+                         void *hip_stream);
+
+/*
+ * Bytes of fp32 workspace ttfa_qk_prologue_bwd needs for the given shape (per-
+ * workgroup partial sums of the norm-weight gradients), or -1 for an invalid shape.
+ */
+long long ttfa_qk_prologue_workspace_bytes(int B, int T, int Hq, int Hkv, int D);
+
+/*
+ * Backward of ttfa_qk_prologue_fwd: dq [B, Hq, T, D], dk/dv [B, Hkv, T, D] (gradients
+ * of its outputs) -> dq_raw, dk_raw, dv_raw in the input layouts, and the fp32 [D]
+ * gradients of the two norm weights (overwritten, not accumulated).  Reads q_raw,
+ * k_raw and the rstd rows the forward wrote.  The weight gradients are summed in a
+ * fixed order (no atomics): results are bitwise reproducible.  Two launches on
+ * hip_stream.
+ */
+int ttfa_qk_prologue_bwd(const void *dq, const void *dk, const void *dv, const void *q_raw,
+                         const void *k_raw, const float *q_norm_w, const float *k_norm_w,
+                         const void *cos, const void *sin, const float *rstd_q,
+                         const float *rstd_k, void *dq_raw, void *dk_raw, void *dv_raw,
+                         float *dq_norm_w, float *dk_norm_w, float *workspace, int B, int T,
+                         int Hq, int Hkv, int D, void *hip_stream);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,8 @@ needs_lib = pytest.mark.skipif(not _lib.LIB_PATH.exists(),
 
 def _declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ttfa_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:\w+\s+)*\w+\s*\*?\s*(ttfa_\w+)\s*\(", text,
+                                 flags=re.M)))
 
 
 def test_header_declares_the_python_binding():
@@ -44,7 +45,7 @@ def test_library_exports_every_declared_symbol():
 
 
 @needs_lib
-@pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7])
+@pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7, -8])
 def test_strerror_names_validation_codes(code):
     msg = _lib.strerror(code)
     assert msg.startswith("ttfa:") and "unknown" not in msg

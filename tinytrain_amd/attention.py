@@ -6,7 +6,9 @@ pretrain.py:226-231.  ``attn_impl``:
 * ``"sdpa"`` -- the eager path, model.py:94-98: optional ``repeat_interleave`` GQA
   expansion, then ``F.scaled_dot_product_attention(is_causal=True)``.
 * ``"hip"``  -- ``flash_attn`` on contiguous q/k/v (the call model.py:92-93 makes for
-  ``"triton"``), backed by libttfa.so.
+  ``"triton"``), backed by libttfa.so.  With ``Attention.fused_prologue`` set, the q/k
+  norms, RoPE and the layout change run as one HIP op (``qk_norm_rope``) instead of the
+  eager expressions.
 
 An unknown name raises ``ValueError`` (no silent fallback).  ``"hip"`` on tensors the
 HIP ops cannot take (CPU tensors, unsupported D) raises too.
@@ -19,6 +21,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .kernels.flash_attn import flash_attn
+from .kernels.qk_prologue import qk_norm_rope
 
 ATTN_IMPLS = ("sdpa", "hip")
 
@@ -87,6 +90,7 @@ class Attention(nn.Module):
         self.k_norm = RMSNorm(head_dim, eps)
         self.enable_gqa = False
         self.attn_impl = "sdpa"
+        self.fused_prologue = False  # "hip" only: q/k norm + RoPE + layout in one HIP op
 
     def forward(self, x, cos, sin):
         B, T, _ = x.shape
@@ -96,6 +100,12 @@ class Attention(nn.Module):
         q = self.q_proj(x).view(B, T, H, dh)
         k = self.k_proj(x).view(B, T, H_kv, dh)
         v = self.v_proj(x).view(B, T, H_kv, dh)
+        if self.fused_prologue and self.attn_impl == "hip":
+            # norm + RoPE + [B, H, T, D] layout in one HIP op (replaces the next 4 lines)
+            q, k, v = qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
+                                   self.q_norm.eps)
+            out = flash_attn(q, k, v)
+            return self.o_proj(out.transpose(1, 2).reshape(B, T, H * dh))
         q, k = self.q_norm(q), self.k_norm(k)
         q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
         cos, sin = cos[:T], sin[:T]

@@ -50,6 +50,7 @@ const char *ttfa_strerror(int code) {
     case TTFA_E_ALIGN: return "ttfa: every pointer must be 16-byte aligned";
     case TTFA_E_DTYPE: return "ttfa: dtype must be TTFA_BF16 or TTFA_F32";
     case TTFA_E_SCALE: return "ttfa: scale must be finite and > 0";
+    case TTFA_E_EPS: return "ttfa: eps must be in [0, 1)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
