@@ -321,6 +321,200 @@ def _copy_probe(mb: float, steps: int, dev) -> int:
     return 0
 
 
+def _ev_time(fn, steps: int, warmup: int) -> float:
+    """Median ms of ``fn`` over ``steps`` calls (HIP events on the current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def _prologue_bench(dev, steps: int, warmup: int) -> int:
+    """Fused q/k norm + RoPE + layout op vs the eager expressions it replaces
+    (model.py:83-93), forward and backward, at the reference model's attention inputs
+    (B=32, T=512, Hq=8, Hkv=2, D=128, bf16).  The op is HBM-bound: its roofline is the
+    bytes it must move over 8 TB/s."""
+    import torch
+
+    from tinytrain_amd.attention import apply_rope, precompute_rope
+    from tinytrain_amd.kernels.qk_prologue import qk_norm_rope_bwd, qk_norm_rope_fwd
+
+    B, T, Hq, Hkv, D, eps = 32, 512, 8, 2, 128, 1e-6
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, T, Hq, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, T, Hkv, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, T, Hkv, D, device=dev, generator=g).to(torch.bfloat16)
+    wq = torch.ones(D, device=dev) + 0.1 * torch.randn(D, device=dev, generator=g)
+    wk = torch.ones(D, device=dev) + 0.1 * torch.randn(D, device=dev, generator=g)
+    cos, sin = (t.to(dev) for t in precompute_rope(D, T, 1e6))
+    gq = torch.randn(B, Hq, T, D, device=dev, generator=g).to(torch.bfloat16)
+    gk = torch.randn(B, Hkv, T, D, device=dev, generator=g).to(torch.bfloat16)
+
+    out = qk_norm_rope_fwd(q, k, v, wq, wk, cos, sin, eps)
+    rq, rk = out[3], out[4]
+    op_fwd = _ev_time(lambda: qk_norm_rope_fwd(q, k, v, wq, wk, cos, sin, eps), steps, warmup)
+    op_bwd = _ev_time(lambda: qk_norm_rope_bwd(gq, gk, gk, q, k, wq, wk, cos, sin, rq, rk),
+                      steps, warmup)
+    # the C ABI alone (tables already bf16, outputs preallocated): the kernels' time
+    from tinytrain_amd import _lib
+
+    lib = _lib.load()
+    cb, sb = cos.to(torch.bfloat16).contiguous(), sin.to(torch.bfloat16).contiguous()
+    qo, ko, vo = (torch.empty_like(t) for t in out[:3])
+    dqr, dkr, dvr = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dwq, dwk = torch.empty_like(wq), torch.empty_like(wk)
+    ws = torch.empty(lib.ttfa_qk_prologue_workspace_bytes(B, T, Hq, Hkv, D) // 4, device=dev)
+    sp = torch.cuda.current_stream(dev).cuda_stream
+
+    def abi_fwd():
+        _lib.check(lib.ttfa_qk_prologue_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), wq.data_ptr(), wk.data_ptr(), cb.data_ptr(),
+            sb.data_ptr(), qo.data_ptr(), ko.data_ptr(), vo.data_ptr(), rq.data_ptr(),
+            rk.data_ptr(), B, T, Hq, Hkv, D, eps, sp))
+
+    def abi_bwd():
+        _lib.check(lib.ttfa_qk_prologue_bwd(
+            gq.data_ptr(), gk.data_ptr(), gk.data_ptr(), q.data_ptr(), k.data_ptr(),
+            wq.data_ptr(), wk.data_ptr(), cb.data_ptr(), sb.data_ptr(), rq.data_ptr(),
+            rk.data_ptr(), dqr.data_ptr(), dkr.data_ptr(), dvr.data_ptr(), dwq.data_ptr(),
+            dwk.data_ptr(), ws.data_ptr(), B, T, Hq, Hkv, D, sp))
+
+    fused_fwd = _ev_time(abi_fwd, steps, warmup)
+    fused_bwd = _ev_time(abi_bwd, steps, warmup)
+
+    def norm(x, w):
+        xf = x.float()
+        return (w * xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+    def eager(qr, kr, vr, wq_, wk_):
+        qn, kn = norm(qr, wq_).transpose(1, 2), norm(kr, wk_).transpose(1, 2)
+        c, s_ = cos[:T], sin[:T]
+        return (apply_rope(qn, c, s_).contiguous(), apply_rope(kn, c, s_).contiguous(),
+                vr.transpose(1, 2).contiguous())
+
+    eager_fwd = _ev_time(lambda: eager(q, k, v, wq, wk), steps, warmup)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v, wq, wk)]
+    outs = eager(*leaves)
+
+    def eager_bwd():
+        torch.autograd.grad(outs, leaves, (gq, gk, gk), retain_graph=True)
+
+    eager_bwd_ms = _ev_time(eager_bwd, steps, warmup)
+    rows_q, rows_kv = B * T * Hq, B * T * Hkv
+    elems = (rows_q + 2 * rows_kv) * D
+    fwd_bytes = 2 * elems * 2 + (rows_q + rows_kv) * 4          # read + write bf16, rstd
+    bwd_bytes = 2 * elems * 2 + (rows_q + rows_kv) * D * 2 + (rows_q + rows_kv) * 4
+    # bwd: read dq/dk/dv + write the three input grads, re-read q_raw/k_raw, read rstd
+    peak = 8000.0
+    line = {
+        "metric": "fused q/k RMSNorm + RoPE + layout prologue, fwd and bwd",
+        "config": {"workload": "reference model attention inputs", "B": B, "T": T, "Hq": Hq,
+                   "Hkv": Hkv, "D": D, "dtype": "bf16"},
+        "fused": {"fwd_ms": round(fused_fwd, 4), "bwd_ms": round(fused_bwd, 4),
+                  "note": "C ABI calls (kernels only; bwd = main pass + weight-gradient sum)"},
+        "fused_op": {"fwd_ms": round(op_fwd, 4), "bwd_ms": round(op_bwd, 4),
+                     "note": "torch custom op: adds the bf16 table conversion and allocation"},
+        "eager_torch": {"fwd_ms": round(eager_fwd, 4), "bwd_ms": round(eager_bwd_ms, 4),
+                        "note": "model.py:83-93 expressions: norm, transpose, apply_rope, "
+                                ".contiguous(); backward through autograd"},
+        "speedup": {"fwd": round(eager_fwd / fused_fwd, 2), "bwd": round(eager_bwd_ms / fused_bwd, 2),
+                    "op_fwd": round(eager_fwd / op_fwd, 2), "op_bwd": round(eager_bwd_ms / op_bwd, 2)},
+        "roofline": {
+            "bound": "hbm", "unit": "GB/s", "peak": peak,
+            "fwd": {"bytes": fwd_bytes, "achieved": round(fwd_bytes / fused_fwd / 1e6, 1),
+                    "frac": round(fwd_bytes / fused_fwd / 1e6 / peak, 4)},
+            "bwd": {"bytes": bwd_bytes, "achieved": round(bwd_bytes / fused_bwd / 1e6, 1),
+                    "frac": round(bwd_bytes / fused_bwd / 1e6 / peak, 4)},
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _model_bench(dev, steps: int, warmup: int, batch: int) -> int:
+    """Whole-model training step (forward, backward, AdamW) of the reference's 112M shape
+    under torch.compile, with attn_impl "sdpa" (enable_gqa, the reference's
+    "compile + GQA" row, docs/results.md:178) vs "hip" vs "hip" + fused prologue; plus
+    the logits of the same weights and tokens under each implementation."""
+    import torch
+
+    from tinytrain_amd.model import ModelConfig, ModelForCausalLM
+
+    torch.manual_seed(0)
+    c = ModelConfig()
+    T = c.max_seq_len
+    model = ModelForCausalLM(c).to(dev)
+    try:
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+        opt_name = "AdamW (fused)"
+    except (RuntimeError, ValueError):
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+        opt_name = "AdamW (foreach)"
+    tok = torch.randint(0, c.vocab_size, (batch, T + 1), device=dev)
+    inp, tgt = tok[:, :-1].contiguous(), tok[:, 1:].contiguous()
+    impls = [("sdpa", False, True), ("hip", False, False), ("hip", True, False)]
+
+    # logits of one set of weights under each implementation (eager, no grad)
+    logits = {}
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        for name, fused, gqa in impls:
+            model.set_attn_impl(name, fused_prologue=fused, enable_gqa=gqa)
+            logits[(name, fused)] = model(inp[:4])[0].float()
+    ref = logits[("sdpa", False)]
+    parity = {f"{n}{'+fused_prologue' if f else ''}": {
+        "max_abs_vs_sdpa": round((l - ref).abs().max().item(), 5),
+        "mean_abs_vs_sdpa": round((l - ref).abs().mean().item(), 6)}
+        for (n, f), l in logits.items() if (n, f) != ("sdpa", False)}
+
+    res = {}
+    for name, fused, gqa in impls:
+        model.set_attn_impl(name, fused_prologue=fused, enable_gqa=gqa)
+        torch._dynamo.reset()
+        cm = torch.compile(model)
+
+        def step():
+            with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                _, loss = cm(inp, tgt)
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+
+        ms = _ev_time(step, steps, warmup)
+        tps = batch * T / (ms * 1e-3)
+        key = f"{name}{'+fused_prologue' if fused else ''}"
+        res[key] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tps, 1),
+                    "model_tflops": round(c.train_flop_per_token(T) * tps / 1e12, 1)}
+        print(f"[model] {key}: {ms:.2f} ms/step, {tps:.0f} tok/s", file=sys.stderr, flush=True)
+    base = res["sdpa"]["tokens_per_s"]
+    for r in res.values():
+        r["vs_sdpa"] = round(r["tokens_per_s"] / base, 3)
+    line = {
+        "metric": "whole-model training tokens/s, attn_impl hip vs sdpa (torch.compile)",
+        "config": {"workload": "reference 112M pretrain shape", "B": batch, "T": T,
+                   "hidden": c.hidden_size, "layers": c.num_hidden_layers,
+                   "Hq": c.num_attention_heads, "Hkv": c.num_key_value_heads,
+                   "D": c.head_dim, "vocab": c.vocab_size, "params": c.params(),
+                   "optimizer": opt_name, "dtype": "bf16 autocast",
+                   "data": "synthetic tokens (seeded)"},
+        "flop_per_token": c.train_flop_per_token(T),
+        "results": res,
+        "logits_parity": parity,
+        "reference_published": {"note": "RTX 4070 Ti Super, docs/results.md:178,184",
+                                "compile+GQA sdpa tok/s": 84638, "compile+GQA triton tok/s": 82634},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,6 +536,13 @@ def main() -> int:
     ap.add_argument("--measure-sq", action="store_true",
                     help="run two rocprofv3 SQ-counter passes over --config (MFMA busy, VALU, "
                          "LDS bank conflicts) and write profiles/sq_counters_<cfg>.txt")
+    ap.add_argument("--prologue", action="store_true",
+                    help="benchmark the fused q/k norm + RoPE + layout op against the eager "
+                         "expressions it replaces (prints its own JSON line)")
+    ap.add_argument("--model", action="store_true",
+                    help="whole-model training benchmark at the reference 112M shape: "
+                         "attn_impl sdpa vs hip vs hip + fused prologue (own JSON line)")
+    ap.add_argument("--model-batch", type=int, default=32)
     ap.add_argument("--no-traffic", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-extras", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -370,6 +571,11 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.copy_probe_mb > 0:
         return _copy_probe(args.copy_probe_mb, args.steps, dev)
+    if args.prologue:
+        return _prologue_bench(dev, args.steps, args.warmup)
+    if args.model:
+        return _model_bench(dev, min(args.steps, 20), min(max(args.warmup, 3), 5),
+                            args.model_batch)
     cfg = CONFIGS[args.config]
     lib = _lib.load()
     B, Hq, Hkv, T, D = cfg.B, cfg.Hq, cfg.Hkv, cfg.T, cfg.D

@@ -243,17 +243,30 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(
   }
 }
 
-// dw_q = sum of the q workgroups' partials, dw_k of the k workgroups', in index order.
+// dw_q = sum of the q workgroups' partials, dw_k of the k workgroups'.  One 1024-thread
+// block per weight vector: thread (slice, col) adds partials slice, slice + S, ... in
+// index order (independent loads, unrolled, so many are in flight), then the S slice
+// sums of each column are added in slice order through LDS: a fixed summation order,
+// so the result is the same on every call.
 template <int D>
-__global__ __launch_bounds__(D) void qk_prologue_dw_kernel(const float *__restrict__ partial,
-                                                           float *__restrict__ dwq,
-                                                           float *__restrict__ dwk, int nq_wg,
-                                                           int nk_wg) {
-  const int col = threadIdx.x;
+__global__ __launch_bounds__(1024) void qk_prologue_dw_kernel(const float *__restrict__ partial,
+                                                              float *__restrict__ dwq,
+                                                              float *__restrict__ dwk, int nq_wg,
+                                                              int nk_wg) {
+  constexpr int S = 1024 / D;
+  __shared__ float red[S][D];
+  const int col = threadIdx.x % D, slice = threadIdx.x / D;
   const int lo = blockIdx.x == 0 ? 0 : nq_wg, n = blockIdx.x == 0 ? nq_wg : nk_wg;
   float acc = 0.f;
-  for (int i = 0; i < n; ++i) acc += partial[(int64_t)(lo + i) * D + col];
-  (blockIdx.x == 0 ? dwq : dwk)[col] = acc;
+#pragma unroll 8
+  for (int i = slice; i < n; i += S) acc += partial[(int64_t)(lo + i) * D + col];
+  red[slice][col] = acc;
+  __syncthreads();
+  if (slice == 0) {
+    float tot = 0.f;
+    for (int j = 0; j < S; ++j) tot += red[j][col];
+    (blockIdx.x == 0 ? dwq : dwk)[col] = tot;
+  }
 }
 
 struct Grid {
@@ -333,7 +346,7 @@ int ttfa_qk_prologue_bwd(const void *dq, const void *dk, const void *dv, const v
   if (rc) return rc;
   if ((rc = check_prologue(B, T, Hq, Hkv, D))) return rc;
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
-  auto go = [&](auto kern, auto dwk_kern, Grid g, int threads) {
+  auto go = [&](auto kern, auto dwk_kern, Grid g) {
     kern<<<dim3((unsigned)(g.nq + g.nk + g.nv)), dim3(256), 0, st>>>(
         (const bf16 *)dq, (const bf16 *)dk, (const bf16 *)dv, (const bf16 *)q_raw,
         (const bf16 *)k_raw, q_norm_w, k_norm_w, (const bf16 *)cos, (const bf16 *)sin, rstd_q,
@@ -341,13 +354,13 @@ int ttfa_qk_prologue_bwd(const void *dq, const void *dk, const void *dv, const v
         g.nk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    dwk_kern<<<dim3(2), dim3(threads), 0, st>>>(workspace, dq_norm_w, dk_norm_w, g.nq, g.nk);
+    dwk_kern<<<dim3(2), dim3(1024), 0, st>>>(workspace, dq_norm_w, dk_norm_w, g.nq, g.nk);
     return (int)hipGetLastError();
   };
   return D == 64 ? go(qk_prologue_bwd_kernel<64>, qk_prologue_dw_kernel<64>,
-                      prologue_grid<64>(B, T, Hq, Hkv), 64)
+                      prologue_grid<64>(B, T, Hq, Hkv))
                  : go(qk_prologue_bwd_kernel<128>, qk_prologue_dw_kernel<128>,
-                      prologue_grid<128>(B, T, Hq, Hkv), 128);
+                      prologue_grid<128>(B, T, Hq, Hkv));
 }
 
 }  // extern "C"
