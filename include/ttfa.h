@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TTFA_ABI_VERSION 2
+#define TTFA_ABI_VERSION 3
 
 enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
 
@@ -99,6 +99,34 @@ int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
                   const float *lse, const float *delta_ws, void *dk, void *dv,
                   int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
                   void *hip_stream);
+
+/*
+ * Packed variable-length (cu_seqlens) causal attention, bf16 only.  Every sequence s
+ * occupies rows cu_seqlens[s] .. cu_seqlens[s+1]-1 of each head and attends causally
+ * within itself only (a block-diagonal causal mask).  No reference kernel has this; it is
+ * the varlen item of the reference's roadmap (README.md:158) on the same kernels as
+ * ttfa_fwd / ttfa_bwd.
+ *
+ *   q, o, dout, dq : [Hq,  total, D] bf16 contiguous (head-major, tokens packed)
+ *   k, v, dk, dv   : [Hkv, total, D] bf16 contiguous
+ *   lse, delta_ws  : [Hq,  total]    fp32
+ *   cu_seqlens     : [n_seq + 1] int32 in device memory, 4-byte aligned, non-decreasing,
+ *                    cu_seqlens[0] = 0, cu_seqlens[n_seq] = total, every length
+ *                    <= max_seqlen.  A sequence with bounds outside 0..total or
+ *                    decreasing is skipped (its rows are not written); rows of a
+ *                    sequence longer than max_seqlen past max_seqlen are not written.
+ * Validation as above, plus TTFA_E_DTYPE for anything but TTFA_BF16 and TTFA_E_SEQ
+ * for n_seq, total or max_seqlen < 1.  Results for each sequence are bitwise those of
+ * ttfa_fwd / ttfa_bwd on that sequence alone (B = 1, T = its length).
+ */
+int ttfa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                    const int *cu_seqlens, int n_seq, int total, int max_seqlen, int Hq, int Hkv,
+                    int D, int dtype, float scale, void *hip_stream);
+
+int ttfa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, float *delta_ws, void *dq, void *dk,
+                    void *dv, const int *cu_seqlens, int n_seq, int total, int max_seqlen,
+                    int Hq, int Hkv, int D, int dtype, float scale, void *hip_stream);
 
 /*
  * Fused attention prologue (bf16 only): q/k RMSNorm + rotate-half RoPE + the layout

@@ -209,6 +209,28 @@ def reference_outputs(q: Tensor, k: Tensor, v: Tensor, do: Tensor,
     return o, lse, dq, dk, dv
 
 
+def varlen_reference(q: Tensor, k: Tensor, v: Tensor, do: Tensor, cu_seqlens,
+                     dtype: torch.dtype = torch.float32):
+    """Packed variable-length attention: q/do [Hq, total, D], k/v [Hkv, total, D], every
+    sequence s (rows cu[s]..cu[s+1]-1) attending causally within itself.  Returns
+    (O, LSE [Hq, total], dQ, dK, dV) by running ``reference_outputs`` (the reference's
+    causal attention, model.py:94-98 / kernels/flash_attn.py:12-217) on each sequence as
+    a batch of one; rows of empty sequences do not exist.  Pinned in tests/test_oracle.py
+    against dense attention over all rows with an explicit block-diagonal causal mask."""
+    cu = [int(x) for x in cu_seqlens]
+    outs = [torch.zeros_like(q, dtype=dtype), torch.zeros(q.shape[:2], dtype=dtype),
+            torch.zeros_like(q, dtype=dtype), torch.zeros_like(k, dtype=dtype),
+            torch.zeros_like(v, dtype=dtype)]
+    for c0, c1 in zip(cu[:-1], cu[1:]):
+        if c1 <= c0:
+            continue
+        o, lse, dq, dk, dv = reference_outputs(q[None, :, c0:c1], k[None, :, c0:c1],
+                                               v[None, :, c0:c1], do[None, :, c0:c1], dtype=dtype)
+        outs[0][:, c0:c1], outs[1][:, c0:c1] = o[0], lse[0]
+        outs[2][:, c0:c1], outs[3][:, c0:c1], outs[4][:, c0:c1] = dq[0], dk[0], dv[0]
+    return tuple(outs)
+
+
 def max_abs(a: Tensor, b: Tensor) -> float:
     """max |a - b| in fp64 (NaN anywhere counts as infinite error)."""
     d = (a.detach().double().cpu() - b.detach().double().cpu()).abs()

@@ -225,3 +225,81 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libttfa.so")
     with pytest.raises(_lib.LibraryNotBuilt, match="missing"):
         _lib.load()
+
+
+# ------------------------------------------------------------------ varlen entry points
+VL = dict(n_seq=3, total=300, max_seqlen=128, Hq=4, Hkv=2, D=64, dtype=_lib.TTFA_BF16,
+          scale=0.125)
+CU = 0x300000  # fake, 4-byte aligned device address of cu_seqlens
+
+
+def _vl_fwd(ptrs=None, cu=CU, **kw):
+    a = {**VL, **kw}
+    p = list(P[:5]) if ptrs is None else ptrs
+    return _lib.load().ttfa_varlen_fwd(*p, cu, a["n_seq"], a["total"], a["max_seqlen"], a["Hq"],
+                                       a["Hkv"], a["D"], a["dtype"], a["scale"], None)
+
+
+def _vl_bwd(ptrs=None, cu=CU, **kw):
+    a = {**VL, **kw}
+    p = list(P[:10]) if ptrs is None else ptrs
+    return _lib.load().ttfa_varlen_bwd(*p, cu, a["n_seq"], a["total"], a["max_seqlen"], a["Hq"],
+                                       a["Hkv"], a["D"], a["dtype"], a["scale"], None)
+
+
+@needs_lib
+@pytest.mark.parametrize("call", [_vl_fwd, _vl_bwd])
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=_lib.TTFA_F32), _lib.E_DTYPE), (dict(D=96), _lib.E_HEAD_DIM),
+    (dict(Hq=3), _lib.E_GROUP), (dict(n_seq=0), _lib.E_SEQ), (dict(total=0), _lib.E_SEQ),
+    (dict(max_seqlen=0), _lib.E_SEQ), (dict(max_seqlen=1 << 24, D=128), _lib.E_SEQ),
+    (dict(scale=0.0), _lib.E_SCALE),
+])
+def test_varlen_abi_validation(call, kw, code):
+    assert call(**kw) == code
+
+
+@needs_lib
+@pytest.mark.parametrize("call,n", [(_vl_fwd, 5), (_vl_bwd, 10)])
+def test_varlen_abi_pointer_checks(call, n):
+    assert call(cu=None) == _lib.E_NULL
+    assert call(cu=CU + 2) == _lib.E_ALIGN
+    for i in range(n):
+        p = list(P[:n])
+        p[i] = None
+        assert call(p) == _lib.E_NULL
+        p = list(P[:n])
+        p[i] = P[i] + 8
+        assert call(p) == _lib.E_ALIGN
+
+
+@pytest.mark.parametrize("bad,msg", [("rank", "3-D"), ("dtype", "bfloat16"),
+                                     ("cu_dtype", "int32"), ("group", "multiple"),
+                                     ("cpu", "ROCm GPU")])
+def test_varlen_input_errors(bad, msg):
+    q = torch.zeros(4, 300, 64, dtype=torch.bfloat16)
+    k = torch.zeros(2, 300, 64, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 100, 300], dtype=torch.int32)
+    if bad == "rank":
+        q = q[None]
+    elif bad == "dtype":
+        q = q.float()
+    elif bad == "cu_dtype":
+        cu = cu.long()
+    elif bad == "group":
+        q = torch.zeros(3, 300, 64, dtype=torch.bfloat16)
+    with pytest.raises(fa.FlashAttnInputError, match=msg):
+        fa.flash_attn_varlen(q, k, k, cu, 200)
+
+
+def test_varlen_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(8, 1000, 128, dtype=torch.bfloat16)
+        k = torch.empty(2, 1000, 128, dtype=torch.bfloat16)
+        cu = torch.empty(5, dtype=torch.int32)
+        o, M = torch.ops.tinytrain.flash_attn_varlen_fwd(q, k, k, cu, 512)
+        assert o.shape == q.shape and M.shape == (8, 1000) and M.dtype == torch.float32
+        dq, dk, dv = torch.ops.tinytrain.flash_attn_varlen_bwd(q, k, k, o, o, M, cu, 512)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape

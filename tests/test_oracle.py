@@ -15,7 +15,8 @@ import torch
 
 from oracle.eager_attention import (attention_bwd, attention_delta, attention_fwd,
                                     brute_force_attention, eager_attention,
-                                    eager_attention_grads, max_abs, reference_outputs)
+                                    eager_attention_grads, max_abs, reference_outputs,
+                                    varlen_reference)
 from tinytrain_amd.workloads import CONFIGS, make_custom, make_inputs
 
 
@@ -211,3 +212,50 @@ def test_make_custom_matches_reference_test_shapes():
     q, k, v, do = make_custom(2, 8, 2, 500, 128, torch.bfloat16, seed=0)
     assert q.shape == (2, 8, 500, 128) and k.shape == (2, 2, 500, 128)
     assert all(t.is_contiguous() and t.dtype == torch.bfloat16 for t in (q, k, v, do))
+
+
+def _block_diag_dense(q, k, v, cu):
+    """Dense fp64 attention over all packed rows with an explicit block-diagonal causal
+    mask (row i may see column j iff both lie in one sequence and j <= i)."""
+    Hq, total, D = q.shape
+    G = Hq // k.shape[0]
+    kk, vv = k.double().repeat_interleave(G, 0), v.double().repeat_interleave(G, 0)
+    seq = torch.zeros(total, dtype=torch.long)
+    for s, (c0, c1) in enumerate(zip(cu[:-1], cu[1:])):
+        seq[c0:c1] = s
+    i = torch.arange(total)
+    allowed = (seq[:, None] == seq[None, :]) & (i[None, :] <= i[:, None])
+    s_ = q.double() @ kk.transpose(-1, -2) / math.sqrt(D)
+    s_ = s_.masked_fill(~allowed, float("-inf"))
+    return torch.softmax(s_, -1) @ vv, torch.logsumexp(s_, -1)
+
+
+def test_varlen_reference_is_block_diagonal_causal_attention():
+    g = torch.Generator().manual_seed(3)
+    cu = [0, 1, 9, 9, 40, 64]  # includes an empty sequence and a length-1 sequence
+    q = torch.randn(4, 64, 64, generator=g)
+    k = torch.randn(2, 64, 64, generator=g)
+    v = torch.randn(2, 64, 64, generator=g)
+    do = torch.randn(4, 64, 64, generator=g)
+    o, lse, dq, dk, dv = varlen_reference(q, k, v, do, cu, dtype=torch.float64)
+    o_d, lse_d = _block_diag_dense(q, k, v, cu)
+    torch.testing.assert_close(o, o_d, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(lse, lse_d, rtol=1e-10, atol=1e-10)
+    # gradients of the dense formulation through autograd
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    o_a, _ = _block_diag_dense(qr, kr, vr, cu)
+    o_a.backward(do.double())
+    for a, b in ((dq, qr.grad), (dk, kr.grad), (dv, vr.grad)):
+        torch.testing.assert_close(a, b, rtol=1e-9, atol=1e-9)
+
+
+def test_planted_mask_leak_across_sequences_is_caught():
+    """Running the packed rows as one causal sequence (the mistake of ignoring
+    cu_seqlens) differs from the block-diagonal reference."""
+    g = torch.Generator().manual_seed(4)
+    cu = [0, 20, 50]
+    q, k, v = (torch.randn(2, 50, 64, generator=g) for _ in range(3))
+    o, *_ = varlen_reference(q, k, v, torch.zeros_like(q), cu, dtype=torch.float64)
+    leak, _ = attention_fwd(q[None], k[None], v[None])
+    assert (o[:, 20:] - leak[0, :, 20:]).abs().max() > 1e-3
+    torch.testing.assert_close(o[:, :20], leak[0, :, :20].to(o.dtype), rtol=1e-10, atol=1e-10)

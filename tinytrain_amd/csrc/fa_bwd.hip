@@ -185,21 +185,24 @@ __device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, con
 }  // namespace
 
 // ---------------------------------------------------------------- pass 1: Delta + dQ
-// Delta and dQ for the 128 query rows of row tile qt of head bh.  Ends with a
+// One query head's rows (q, o, dout, dq: T rows of D; lse, delta: T values) and its KV
+// head's rows (k, v) for one sequence.
+struct DqHead {
+  const bf16 *q, *k, *v, *o, *dout;
+  const float *lse;
+  float *delta;
+  bf16 *dq;
+  int T;
+};
+
+// Delta and dQ for the 128 query rows of row tile qt of one head.  Ends with a
 // workgroup barrier, so the caller may reuse the LDS ring right away.
 template <int D>
-__device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
-                                        const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-                                        const bf16 *__restrict__ O, const bf16 *__restrict__ dO,
-                                        const float *__restrict__ LSE, float *__restrict__ Delta,
-                                        bf16 *__restrict__ dQ, int bh, int qt, int Hq, int Hkv,
-                                        int T, float scale_log2, float scale, int work_left,
-                                        int work_max) {
+__device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, float scale_log2,
+                                        float scale, int work_left, int work_max) {
   using P = DqTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  const int G = Hq / Hkv;
-  const int b = bh / Hq, h = bh - b * Hq;
-  const int64_t kv_head = (int64_t)b * Hkv + h / G;
+  const int T = hd.T;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, lg = lane >> 5;
@@ -207,12 +210,11 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const int qrow = q0 + lq;
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const int64_t qbase = (int64_t)bh * T * D;
-  const auto rq = make_rsrc(Q + qbase, head_bytes);
-  const auto ro = make_rsrc(O + qbase, head_bytes);
-  const auto rdo = make_rsrc(dO + qbase, head_bytes);
-  const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
-  const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
+  const auto rq = make_rsrc(hd.q, head_bytes);
+  const auto ro = make_rsrc(hd.o, head_bytes);
+  const auto rdo = make_rsrc(hd.dout, head_bytes);
+  const auto rk = make_rsrc(hd.k, head_bytes);
+  const auto rv = make_rsrc(hd.v, head_bytes);
 
   // Global -> LDS without registers: lane l of the wave's 1 KB block e0 writes physical
   // chunk (e0 + l) % CH of row (e0 + l) / CH, which holds logical chunk phys ^ swizzle(row).
@@ -241,8 +243,8 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const float delta = xhalf_sum(dpart);
   float lse_t = 0.f;
   if (qrow < T) {
-    lse_t = LSE[(int64_t)bh * T + qrow] * kLog2e;
-    if (lg == 0) Delta[(int64_t)bh * T + qrow] = delta;
+    lse_t = hd.lse[qrow] * kLog2e;
+    if (lg == 0) hd.delta[qrow] = delta;
   }
   f32x16 ndelta;
 #pragma unroll
@@ -274,7 +276,7 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const bf16 *__restrict__ Q,
 
   // The loop's last barrier freed the LDS ring: each wave stages its dQ tile in its own
   // 32*D slice of it for row-contiguous stores.
-  store_rows<D>(dqacc, scale, lds + wave * 32 * D, dQ + (int64_t)bh * T * D, q0, T, lane);
+  store_rows<D>(dqacc, scale, lds + wave * 32 * D, hd.dq, q0, T, lane);
   __syncthreads();  // the ring is free again for the caller
 }
 
@@ -294,30 +296,68 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
   auto work = [&](int qt) { return qt < 0 ? 0 : min(n_kt, (qt + 1) * (P::BM / P::BN)); };
   const int w1 = work(w.first), w2 = work(w.second);
   const int wmax = paired ? work(n_tiles - 1) + work(0) : work(n_tiles - 1);
-  dq_rows<D>(smem, Q, K, V, O, dO, LSE, Delta, dQ, w.bh, w.first, Hq, Hkv, T, scale_log2, scale,
-             w1 + w2, wmax);
-  if (w.second >= 0)
-    dq_rows<D>(smem, Q, K, V, O, dO, LSE, Delta, dQ, w.bh, w.second, Hq, Hkv, T, scale_log2,
-               scale, w2, wmax);
+  const int G = Hq / Hkv;
+  const int b = w.bh / Hq, h = w.bh - b * Hq;
+  const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D, qb = w.bh * hs;
+  const DqHead hd{Q + qb, K + kvh * hs, V + kvh * hs, O + qb, dO + qb,
+                  LSE + (int64_t)w.bh * T, Delta + (int64_t)w.bh * T, dQ + qb, T};
+  dq_rows<D>(smem, hd, w.first, scale_log2, scale, w1 + w2, wmax);
+  if (w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
+}
+
+// Packed variable-length sequences ([H, total, D], sequence s at rows cu_seqlens[s] ..
+// cu_seqlens[s+1]-1 of every head; LSE / Delta [H, total]).  Workgroup -> (tile rank,
+// sequence, query head), rank-major, longest row tiles first; invalid sequence bounds
+// are skipped.
+template <int D>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq_varlen_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    float *__restrict__ Delta, bf16 *__restrict__ dQ, const int *__restrict__ cu_seqlens,
+    int n_seq, int total, int Hq, int Hkv, int max_tiles, float scale_log2, float scale) {
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  using P = DqTile<D>;
+  const int per_rank = n_seq * Hq;
+  const int rank = blockIdx.x / per_rank, rem = blockIdx.x - rank * per_rank;
+  const int s = rem / Hq, h = rem - s * Hq;
+  const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
+  if (c0 < 0 || c1 < c0 || c1 > total) return;
+  const int T = c1 - c0;
+  const int n_tiles = (T + P::BM - 1) / P::BM;
+  if (rank >= n_tiles) return;
+  const int qt = n_tiles - 1 - rank;
+  const int n_kt = (T + P::BN - 1) / P::BN;
+  const int wmax = max_tiles * (P::BM / P::BN);
+  const int hk = h / (Hq / Hkv);
+  const int64_t qb = ((int64_t)h * total + c0) * D, kb = ((int64_t)hk * total + c0) * D;
+  const int64_t rb = (int64_t)h * total + c0;
+  const DqHead hd{Q + qb, K + kb, V + kb, O + qb, dO + qb, LSE + rb, Delta + rb, dQ + qb, T};
+  dq_rows<D>(smem, hd, qt, scale_log2, scale, min(n_kt, (qt + 1) * (P::BM / P::BN)), wmax);
 }
 
 // ---------------------------------------------------------------- pass 2: dK, dV
-// dK and dV for the 128 keys of key tile kt of kv head bhk (= batch * Hkv + kv head),
-// reduced over the head's query-head group.  Ends with a workgroup barrier, so the
-// caller may reuse the LDS ring right away.
+// One KV head's rows (k, v, dk, dv: T rows of D) for one sequence, and the G query heads
+// that read it: query head g's q / dout rows at q + g * head_stride (elements), its lse /
+// delta values at lse + g * row_stride.
+struct DkvHead {
+  const bf16 *k, *v;
+  bf16 *dk, *dv;
+  const bf16 *q, *dout;
+  const float *lse, *delta;
+  int64_t head_stride, row_stride;
+  int G, T;
+};
+
+// dK and dV for the 128 keys of key tile kt of one KV head, reduced over the head's
+// query-head group.  Ends with a workgroup barrier, so the caller may reuse the LDS ring
+// right away.
 template <int D>
-__device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
-                                          const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-                                          const bf16 *__restrict__ dO, const float *__restrict__ LSE,
-                                          const float *__restrict__ Delta, bf16 *__restrict__ dK,
-                                          bf16 *__restrict__ dV, int bhk, int kt, int Hq, int Hkv,
-                                          int T, float scale_log2, float scale, int work_left,
-                                          int work_max) {
+__device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, float scale_log2,
+                                          float scale, int work_left, int work_max) {
   using P = DkvTile<D>;
   constexpr int BNK = P::BNK, BMQ = P::BMQ, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   float *const ldsf = reinterpret_cast<float *>(lds + 2 * 2 * BMQ * D);
-  const int G = Hq / Hkv;
-  const int b = bhk / Hkv, hk = bhk - b * Hkv;
+  const int G = hd.G, T = hd.T;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, lg = lane >> 5;
@@ -325,9 +365,8 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
   const int krow = k0w + lq;
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const int64_t kvbase = (int64_t)bhk * T * D;
-  const auto rk = make_rsrc(K + kvbase, head_bytes);
-  const auto rv = make_rsrc(V + kvbase, head_bytes);
+  const auto rk = make_rsrc(hd.k, head_bytes);
+  const auto rv = make_rsrc(hd.v, head_bytes);
 
   // K^T, V^T as B operands: lane (key lq, lg) slot s of step kk = row krow, d = 16kk+8lg+s.
   bf16x8 kf[KK], vf[KK];
@@ -358,9 +397,9 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
       ld_qt = qt_lo;
       ++ld_g;
     }
-    const int64_t bhq = (int64_t)b * Hq + hk * G + g;
-    const auto rq = make_rsrc(Q + bhq * T * D, head_bytes);
-    const auto rdo = make_rsrc(dO + bhq * T * D, head_bytes);
+    const auto rq = make_rsrc(hd.q + g * hd.head_stride, head_bytes);
+    const auto rdo = make_rsrc(hd.dout + g * hd.head_stride, head_bytes);
+    const float *lse_g = hd.lse + g * hd.row_stride, *delta_g = hd.delta + g * hd.row_stride;
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
@@ -371,7 +410,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
     if (tid < 2 * BMQ) {
       const int r = qt * BMQ + (tid & (BMQ - 1));
       fl = 0.f;
-      if (r < T) fl = tid < BMQ ? -LSE[bhq * T + r] * inv_scale : -Delta[bhq * T + r];
+      if (r < T) fl = tid < BMQ ? -lse_g[r] * inv_scale : -delta_g[r];
     }
   };
   auto stage_rows = [&](int stage) {
@@ -424,8 +463,8 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const bf16 *__restrict__ Q,
 
   // The loop's last barrier freed the LDS ring: each wave stages its dK and dV tiles in
   // its own two 32*D slices of it for row-contiguous stores.
-  store_rows<D>(dkacc, scale, lds + wave * 64 * D, dK + kvbase, k0w, T, lane);
-  store_rows<D>(dvacc, 1.f, lds + wave * 64 * D + 32 * D, dV + kvbase, k0w, T, lane);
+  store_rows<D>(dkacc, scale, lds + wave * 64 * D, hd.dk, k0w, T, lane);
+  store_rows<D>(dvacc, 1.f, lds + wave * 64 * D + 32 * D, hd.dv, k0w, T, lane);
   __syncthreads();  // the ring is free again for the caller
 }
 
@@ -447,11 +486,42 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
   auto work = [&](int kt) { return kt < 0 ? 0 : G * (n_qt - kt * (P::BNK / P::BMQ)); };
   const int w1 = work(w.first), w2 = work(w.second);
   const int wmax = paired ? work(0) + work(n_ktiles - 1) : work(0);
-  dkdv_rows<D>(smem, Q, K, V, dO, LSE, Delta, dK, dV, w.bh, w.first, Hq, Hkv, T, scale_log2, scale,
-               w1 + w2, wmax);
-  if (w.second >= 0)
-    dkdv_rows<D>(smem, Q, K, V, dO, LSE, Delta, dK, dV, w.bh, w.second, Hq, Hkv, T, scale_log2,
-                 scale, w2, wmax);
+  const int b = w.bh / Hkv, hk = w.bh - b * Hkv;
+  const int64_t hs = (int64_t)T * D, kvb = w.bh * hs, q0 = (int64_t)b * Hq + hk * G;
+  const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs, dO + q0 * hs,
+                   LSE + q0 * T, Delta + q0 * T, hs, T, G, T};
+  dkdv_rows<D>(smem, hd, w.first, scale_log2, scale, w1 + w2, wmax);
+  if (w.second >= 0) dkdv_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
+}
+
+// Packed variable-length sequences (layouts as for the varlen dQ pass).  Workgroup ->
+// (key tile rank, sequence, KV head), rank-major; key tile 0 of a sequence sees the most
+// query rows, so rank r is key tile r.  Invalid sequence bounds are skipped.
+template <int D>
+__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV,
+    const int *__restrict__ cu_seqlens, int n_seq, int total, int Hq, int Hkv, int max_ktiles,
+    float scale_log2, float scale) {
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  using P = DkvTile<D>;
+  const int per_rank = n_seq * Hkv;
+  const int kt = blockIdx.x / per_rank, rem = blockIdx.x - kt * per_rank;
+  const int s = rem / Hkv, hk = rem - s * Hkv;
+  const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
+  if (c0 < 0 || c1 < c0 || c1 > total) return;
+  const int T = c1 - c0;
+  if (kt >= (T + P::BNK - 1) / P::BNK) return;
+  const int G = Hq / Hkv;
+  const int n_qt = (T + P::BMQ - 1) / P::BMQ;
+  const int wmax = G * max_ktiles * (P::BNK / P::BMQ);
+  const int64_t hs = (int64_t)total * D, kvb = (int64_t)hk * hs + (int64_t)c0 * D;
+  const int64_t q0 = (int64_t)hk * G;
+  const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs + (int64_t)c0 * D,
+                   dO + q0 * hs + (int64_t)c0 * D, LSE + q0 * total + c0,
+                   Delta + q0 * total + c0, hs, total, G, T};
+  dkdv_rows<D>(smem, hd, kt, scale_log2, scale, G * (n_qt - kt * (P::BNK / P::BMQ)), wmax);
 }
 
 template <typename Kern>
@@ -498,6 +568,63 @@ static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const
                                      (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv, B,
                                      Hq, Hkv, T, scale * kLog2e, scale, (int)paired);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_dq_varlen(const void *q, const void *k, const void *v, const void *o,
+                                   const void *dout, const float *lse, float *delta, void *dq,
+                                   const int *cu_seqlens, int n_seq, int total, int max_seqlen,
+                                   int Hq, int Hkv, float scale, hipStream_t stream) {
+  const int max_tiles = (max_seqlen + DqTile<D>::BM - 1) / DqTile<D>::BM;
+  constexpr size_t lds = DqTile<D>::LDS_BYTES;
+  auto kern = fa_bwd_dq_varlen_bf16_kernel<D>;
+  if (lds > 65536) {
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid((unsigned)((int64_t)max_tiles * n_seq * Hq)), block(256);
+  kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                     (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
+                                     cu_seqlens, n_seq, total, Hq, Hkv, max_tiles, scale * kLog2e,
+                                     scale);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_dkdv_varlen(const void *q, const void *k, const void *v,
+                                     const void *dout, const float *lse, const float *delta,
+                                     void *dk, void *dv, const int *cu_seqlens, int n_seq,
+                                     int total, int max_seqlen, int Hq, int Hkv, float scale,
+                                     hipStream_t stream) {
+  const int max_ktiles = (max_seqlen + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
+  constexpr size_t lds = DkvTile<D>::LDS_BYTES;
+  auto kern = fa_bwd_dkdv_varlen_bf16_kernel<D>;
+  if (lds > 65536) {
+    hipError_t e = allow_lds(kern, lds);
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid((unsigned)((int64_t)max_ktiles * n_seq * Hkv)), block(256);
+  kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                     (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv,
+                                     cu_seqlens, n_seq, total, Hq, Hkv, max_ktiles,
+                                     scale * kLog2e, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_varlen_bf16(const void *q, const void *k, const void *v, const void *o,
+                                  const void *dout, const float *lse, float *delta, void *dq,
+                                  void *dk, void *dv, const int *cu_seqlens, int n_seq,
+                                  int total, int max_seqlen, int Hq, int Hkv, int D, float scale,
+                                  hipStream_t stream) {
+  hipError_t e = D == 64 ? launch_dq_varlen<64>(q, k, v, o, dout, lse, delta, dq, cu_seqlens,
+                                                n_seq, total, max_seqlen, Hq, Hkv, scale, stream)
+                         : launch_dq_varlen<128>(q, k, v, o, dout, lse, delta, dq, cu_seqlens,
+                                                 n_seq, total, max_seqlen, Hq, Hkv, scale, stream);
+  if (e != hipSuccess) return e;
+  return D == 64 ? launch_dkdv_varlen<64>(q, k, v, dout, lse, delta, dk, dv, cu_seqlens, n_seq,
+                                          total, max_seqlen, Hq, Hkv, scale, stream)
+                 : launch_dkdv_varlen<128>(q, k, v, dout, lse, delta, dk, dv, cu_seqlens, n_seq,
+                                           total, max_seqlen, Hq, Hkv, scale, stream);
 }
 
 hipError_t launch_bwd_dq_bf16(const void *q, const void *k, const void *v, const void *o,

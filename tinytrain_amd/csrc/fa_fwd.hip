@@ -114,20 +114,23 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
 
 }  // namespace
 
-// All 128 query rows of row tile qt of head bh: online softmax over its key tiles.
+// One query head's rows and its KV head's rows for one sequence: T rows of D starting at
+// q / k / v / o, and T LSE values at lse.
+struct FwdHead {
+  const bf16 *q, *k, *v;
+  bf16 *o;
+  float *lse;
+  int T;
+};
+
+// All 128 query rows of row tile qt of one head: online softmax over its key tiles.
 // Ends with a workgroup barrier, so the caller may reuse the LDS ring right away.
 template <int D>
-__device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
-                                         const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
-                                         const bf16 *__restrict__ V, bf16 *__restrict__ O,
-                                         float *__restrict__ LSE, int bh, int qt, int Hq,
-                                         int Hkv, int T, float scale_log2, int work_left,
-                                         int work_max) {
+__device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], const FwdHead &hd,
+                                         int qt, float scale_log2, int work_left, int work_max) {
   using P = FwdTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  const int G = Hq / Hkv;
-  const int b = bh / Hq, h = bh - b * Hq;
-  const int64_t kv_head = (int64_t)b * Hkv + h / G;
+  const int T = hd.T;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, lg = lane >> 5;
@@ -135,9 +138,9 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
   const int qrow = q0 + lq;
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const auto rq = make_rsrc(Q + (int64_t)bh * T * D, head_bytes);
-  const auto rk = make_rsrc(K + kv_head * T * D, head_bytes);
-  const auto rv = make_rsrc(V + kv_head * T * D, head_bytes);
+  const auto rq = make_rsrc(hd.q, head_bytes);
+  const auto rk = make_rsrc(hd.k, head_bytes);
+  const auto rv = make_rsrc(hd.v, head_bytes);
 
   // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
   // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
@@ -192,8 +195,8 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D],
   // The loop's last barrier freed the LDS ring: each wave stages its O tile in its own
   // 32*D slice of it for row-contiguous stores.
   const float l = xhalf_sum(l_part);
-  store_rows<D>(oacc, 1.f / l, &lds[0][0][0] + wave * 32 * D, O + (int64_t)bh * T * D, q0, T, lane);
-  if (qrow < T && lg == 0) LSE[(int64_t)bh * T + qrow] = (m_t + __log2f(l)) * kLn2;
+  store_rows<D>(oacc, 1.f / l, &lds[0][0][0] + wave * 32 * D, hd.o, q0, T, lane);
+  if (qrow < T && lg == 0) hd.lse[qrow] = (m_t + __log2f(l)) * kLn2;
   __syncthreads();  // the ring is free again for the caller
 }
 
@@ -212,8 +215,43 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
   auto work = [&](int qt) { return qt < 0 ? 0 : min(n_kt, (qt + 1) * (P::BM / P::BN)); };
   const int w1 = work(w.first), w2 = work(w.second);
   const int wmax = paired ? work(n_tiles - 1) + work(0) : work(n_tiles - 1);
-  fwd_rows<D>(lds, Q, K, V, O, LSE, w.bh, w.first, Hq, Hkv, T, scale_log2, w1 + w2, wmax);
-  if (w.second >= 0) fwd_rows<D>(lds, Q, K, V, O, LSE, w.bh, w.second, Hq, Hkv, T, scale_log2, w2, wmax);
+  const int G = Hq / Hkv;
+  const int b = w.bh / Hq, h = w.bh - b * Hq;
+  const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D;
+  const FwdHead hd{Q + w.bh * hs, K + kvh * hs, V + kvh * hs, O + w.bh * hs,
+                   LSE + (int64_t)w.bh * T, T};
+  fwd_rows<D>(lds, hd, w.first, scale_log2, w1 + w2, wmax);
+  if (w.second >= 0) fwd_rows<D>(lds, hd, w.second, scale_log2, w2, wmax);
+}
+
+// Packed variable-length sequences ([H, total, D] per tensor, sequence s at rows
+// cu_seqlens[s] .. cu_seqlens[s+1]-1 of every head, causal within each sequence).
+// Workgroup -> (tile rank, sequence, query head), rank-major, so every sequence's
+// longest row tiles (rank 0 = its last tile) are dispatched first; a rank past a
+// sequence's tile count exits at once.  Sequences whose bounds are not
+// 0 <= cu[s] <= cu[s+1] <= total are skipped (nothing is read or written for them).
+template <int D>
+__global__ __launch_bounds__(256, 2) void fa_fwd_varlen_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    bf16 *__restrict__ O, float *__restrict__ LSE, const int *__restrict__ cu_seqlens,
+    int n_seq, int total, int Hq, int Hkv, int max_tiles, float scale_log2) {
+  using P = FwdTile<D>;
+  __shared__ __attribute__((aligned(16))) bf16 lds[2][2][P::BN * D];
+  const int per_rank = n_seq * Hq;
+  const int rank = blockIdx.x / per_rank, rem = blockIdx.x - rank * per_rank;
+  const int s = rem / Hq, h = rem - s * Hq;
+  const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
+  if (c0 < 0 || c1 < c0 || c1 > total) return;
+  const int T = c1 - c0;
+  const int n_tiles = (T + P::BM - 1) / P::BM;
+  if (rank >= n_tiles) return;
+  const int qt = n_tiles - 1 - rank;
+  const int n_kt = (T + P::BN - 1) / P::BN;
+  const int wmax = min((max_tiles * P::BM + P::BN - 1) / P::BN, max_tiles * (P::BM / P::BN));
+  const int hk = h / (Hq / Hkv);
+  const int64_t qb = ((int64_t)h * total + c0) * D, kb = ((int64_t)hk * total + c0) * D;
+  const FwdHead hd{Q + qb, K + kb, V + kb, O + qb, LSE + (int64_t)h * total + c0, T};
+  fwd_rows<D>(lds, hd, qt, scale_log2, min(n_kt, (qt + 1) * (P::BM / P::BN)), wmax);
 }
 
 hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
@@ -230,6 +268,22 @@ hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o,
   };
   return D == 64 ? go(fa_fwd_bf16_kernel<64>, resident_slots<fa_fwd_bf16_kernel<64>>(256, 0))
                  : go(fa_fwd_bf16_kernel<128>, resident_slots<fa_fwd_bf16_kernel<128>>(256, 0));
+}
+
+hipError_t launch_fwd_varlen_bf16(const void *q, const void *k, const void *v, void *o,
+                                  float *lse, const int *cu_seqlens, int n_seq, int total,
+                                  int max_seqlen, int Hq, int Hkv, int D, float scale,
+                                  hipStream_t stream) {
+  const int max_tiles = (max_seqlen + FwdTile<64>::BM - 1) / FwdTile<64>::BM;
+  const dim3 grid((unsigned)((int64_t)max_tiles * n_seq * Hq)), block(256);
+  const float sl2 = scale * kLog2e;
+  auto go = [&](auto kern) {
+    kern<<<grid, block, 0, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
+                                     (bf16 *)o, lse, cu_seqlens, n_seq, total, Hq, Hkv, max_tiles,
+                                     sl2);
+    return hipGetLastError();
+  };
+  return D == 64 ? go(fa_fwd_varlen_bf16_kernel<64>) : go(fa_fwd_varlen_bf16_kernel<128>);
 }
 
 }  // namespace ttfa

@@ -17,6 +17,18 @@ hipError_t launch_bwd_dkdv_bf16(const void *q, const void *k, const void *v, con
                                 int B, int Hq, int Hkv, int T, int D, float scale,
                                 hipStream_t stream);
 
+// Packed variable-length sequences, bf16: q/o [Hq, total, D], k/v [Hkv, total, D],
+// lse/delta [Hq, total]; cu_seqlens [n_seq + 1] int32 on the device.
+hipError_t launch_fwd_varlen_bf16(const void *q, const void *k, const void *v, void *o,
+                                  float *lse, const int *cu_seqlens, int n_seq, int total,
+                                  int max_seqlen, int Hq, int Hkv, int D, float scale,
+                                  hipStream_t stream);
+hipError_t launch_bwd_varlen_bf16(const void *q, const void *k, const void *v, const void *o,
+                                  const void *dout, const float *lse, float *delta, void *dq,
+                                  void *dk, void *dv, const int *cu_seqlens, int n_seq,
+                                  int total, int max_seqlen, int Hq, int Hkv, int D, float scale,
+                                  hipStream_t stream);
+
 hipError_t launch_fwd_f32(const void *q, const void *k, const void *v, void *o, float *lse,
                           int B, int Hq, int Hkv, int T, int D, float scale, hipStream_t stream);
 hipError_t launch_bwd_dq_f32(const void *q, const void *k, const void *v, const void *o,

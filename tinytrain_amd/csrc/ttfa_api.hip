@@ -26,6 +26,21 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, float scale) {
   return TTFA_OK;
 }
 
+// Packed variable-length sequences: bf16 only; n_seq, total, max_seqlen >= 1; per-
+// sequence byte extents within the 32-bit buffer descriptors; grids within int range.
+int check_varlen(int n_seq, int total, int max_seqlen, int Hq, int Hkv, int D, int dtype,
+                 float scale) {
+  if (dtype != TTFA_BF16) return TTFA_E_DTYPE;
+  if (D != 64 && D != 128) return TTFA_E_HEAD_DIM;
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return TTFA_E_GROUP;
+  if (n_seq < 1 || total < 1 || max_seqlen < 1) return TTFA_E_SEQ;
+  if ((int64_t)max_seqlen * D * 2 > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if ((int64_t)((max_seqlen + 127) / 128) * n_seq * Hq > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if ((int64_t)Hq * total > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if (!(scale > 0.f) || !isfinite(scale)) return TTFA_E_SCALE;
+  return TTFA_OK;
+}
+
 int check_ptrs(const void *const *ptrs, int n) {
   for (int i = 0; i < n; ++i)
     if (ptrs[i] == nullptr) return TTFA_E_NULL;
@@ -98,6 +113,35 @@ int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
           ? ttfa::launch_bwd_dkdv_bf16(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, scale, s)
           : ttfa::launch_bwd_dkdv_f32(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, scale, s);
   return static_cast<int>(e);
+}
+
+int ttfa_varlen_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+                    const int *cu_seqlens, int n_seq, int total, int max_seqlen, int Hq, int Hkv,
+                    int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_varlen(n_seq, total, max_seqlen, Hq, Hkv, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, o, lse};
+  if ((rc = check_ptrs(ptrs, 5))) return rc;
+  if (cu_seqlens == nullptr) return TTFA_E_NULL;
+  if (reinterpret_cast<uintptr_t>(cu_seqlens) & 3u) return TTFA_E_ALIGN;
+  return static_cast<int>(ttfa::launch_fwd_varlen_bf16(q, k, v, o, lse, cu_seqlens, n_seq, total,
+                                                       max_seqlen, Hq, Hkv, D, scale,
+                                                       static_cast<hipStream_t>(hip_stream)));
+}
+
+int ttfa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, float *delta_ws, void *dq, void *dk,
+                    void *dv, const int *cu_seqlens, int n_seq, int total, int max_seqlen,
+                    int Hq, int Hkv, int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_varlen(n_seq, total, max_seqlen, Hq, Hkv, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k, v, o, dout, lse, delta_ws, dq, dk, dv};
+  if ((rc = check_ptrs(ptrs, 10))) return rc;
+  if (cu_seqlens == nullptr) return TTFA_E_NULL;
+  if (reinterpret_cast<uintptr_t>(cu_seqlens) & 3u) return TTFA_E_ALIGN;
+  return static_cast<int>(ttfa::launch_bwd_varlen_bf16(
+      q, k, v, o, dout, lse, delta_ws, dq, dk, dv, cu_seqlens, n_seq, total, max_seqlen, Hq, Hkv,
+      D, scale, static_cast<hipStream_t>(hip_stream)));
 }
 
 int ttfa_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
