@@ -440,6 +440,101 @@ def _prologue_bench(dev, steps: int, warmup: int) -> int:
     return 0
 
 
+def _varlen_bench(dev, steps: int, warmup: int) -> int:
+    """Packed variable-length causal attention at C2's head shape (Hq = Hkv = 12, D = 64)
+    and token count (16 x 1024): seeded lengths 64..2048, fwd and bwd through the C ABI,
+    algorithmic FLOPs summed per sequence (2 * Hq * len^2 * D forward, x2.5 backward)."""
+    import torch
+
+    from tinytrain_amd import _lib
+
+    Hq = Hkv = 12
+    D, total_target = 64, 16 * 1024
+    g = torch.Generator().manual_seed(0)
+    lens = []
+    while sum(lens) < total_target:
+        lens.append(int(torch.randint(64, 2049, (1,), generator=g)))
+    lens[-1] -= sum(lens) - total_target
+    if lens[-1] <= 0:
+        lens.pop()
+    total = sum(lens)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32, device=dev)
+    mk = lambda h: torch.randn(h, total, D, device=dev).to(torch.bfloat16)
+    q, k, v, do = mk(Hq), mk(Hkv), mk(Hkv), mk(Hq)
+    o, lse = torch.empty_like(q), torch.empty(Hq, total, device=dev)
+    delta = torch.empty(Hq, total, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    lib = _lib.load()
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    scale = 1.0 / math.sqrt(D)
+    args = (cu.data_ptr(), len(lens), total, max(lens), Hq, Hkv, D, _lib.TTFA_BF16, scale, sp)
+
+    def fwd():
+        _lib.check(lib.ttfa_varlen_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                       lse.data_ptr(), *args))
+
+    def bwd():
+        _lib.check(lib.ttfa_varlen_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                       do.data_ptr(), lse.data_ptr(), delta.data_ptr(),
+                                       dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *args))
+
+    fwd()
+    f_ms, b_ms = _ev_time(fwd, steps, warmup), _ev_time(bwd, steps, warmup)
+    fwd_flop = sum(2.0 * Hq * L * L * D for L in lens)
+    line = {
+        "metric": "packed varlen causal attention fwd / bwd TFLOP/s (cu_seqlens)",
+        "config": {"workload": "C2 heads and token count, seeded lengths 64..2048",
+                   "Hq": Hq, "Hkv": Hkv, "D": D, "total_tokens": total, "n_seq": len(lens),
+                   "max_seqlen": max(lens), "dtype": "bf16"},
+        "fwd": {"ms": round(f_ms, 4), "tflops": round(fwd_flop / f_ms / 1e9, 1)},
+        "bwd": {"ms": round(b_ms, 4), "tflops": round(2.5 * fwd_flop / b_ms / 1e9, 1)},
+        "fwd_bwd_tflops": round(3.5 * fwd_flop / (f_ms + b_ms) / 1e9, 1),
+        "frac_of_peak": round(3.5 * fwd_flop / (f_ms + b_ms) / 1e9 / PEAK_BF16_TFLOPS, 4),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _decode_bench(dev, steps: int, warmup: int) -> int:
+    """KV-cache decode (one new token per sequence) at the C4/C5 head shape (Hq 16,
+    Hkv 8, D 128): a rollout-sized batch (B 32, caches of 4096) and one long sequence
+    (B 1, 16384).  HBM-bound: the roofline is the cache bytes read (K and V of every
+    cached key once) over 8 TB/s."""
+    import torch
+
+    from tinytrain_amd import _lib
+
+    lib = _lib.load()
+    sp = torch.cuda.current_stream(dev).cuda_stream
+    out = []
+    for B, L in ((32, 4096), (1, 16384), (128, 1024)):
+        Hq, Hkv, D, Tq = 16, 8, 128, 1
+        q = torch.randn(B, Hq, Tq, D, device=dev).to(torch.bfloat16)
+        kc = torch.randn(B, Hkv, L, D, device=dev).to(torch.bfloat16)
+        vc = torch.randn(B, Hkv, L, D, device=dev).to(torch.bfloat16)
+        lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+        o = torch.empty_like(q)
+        lse = torch.empty(B, Hq, Tq, device=dev)
+        ws = torch.empty(lib.ttfa_decode_workspace_bytes(B, Hq, Hkv, Tq, L, D) // 4 + 4, device=dev)
+
+        def call():
+            _lib.check(lib.ttfa_decode_fwd(q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                           lens.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                           ws.data_ptr(), B, Hq, Hkv, Tq, L, D, _lib.TTFA_BF16,
+                                           1.0 / math.sqrt(D), sp))
+
+        ms = _ev_time(call, steps, warmup)
+        nbytes = 2 * B * Hkv * L * D * 2 + 2 * B * Hq * Tq * D * 2
+        out.append({"B": B, "Hq": Hq, "Hkv": Hkv, "D": D, "Tq": Tq, "cache_len": L,
+                    "ms": round(ms, 4), "cache_bytes": nbytes,
+                    "GB_per_s": round(nbytes / ms / 1e6, 1),
+                    "frac_of_hbm_peak": round(nbytes / ms / 1e6 / 8000.0, 4)})
+    print(json.dumps({"metric": "KV-cache decode attention, HBM GB/s (split + merge launches)",
+                      "roofline": {"bound": "hbm", "peak": 8000.0, "unit": "GB/s"},
+                      "cases": out}), flush=True)
+    return 0
+
+
 def _model_bench(dev, steps: int, warmup: int, batch: int) -> int:
     """Whole-model training step (forward, backward, AdamW) of the reference's 112M shape
     under torch.compile, with attn_impl "sdpa" (enable_gqa, the reference's
@@ -543,6 +638,12 @@ def main() -> int:
                     help="whole-model training benchmark at the reference 112M shape: "
                          "attn_impl sdpa vs hip vs hip + fused prologue (own JSON line)")
     ap.add_argument("--model-batch", type=int, default=32)
+    ap.add_argument("--decode", action="store_true",
+                    help="KV-cache decode attention bandwidth at the C4/C5 head shape "
+                         "(own JSON line)")
+    ap.add_argument("--varlen", action="store_true",
+                    help="packed variable-length attention at C2's heads and token count "
+                         "(own JSON line)")
     ap.add_argument("--no-traffic", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--no-extras", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -573,6 +674,10 @@ def main() -> int:
         return _copy_probe(args.copy_probe_mb, args.steps, dev)
     if args.prologue:
         return _prologue_bench(dev, args.steps, args.warmup)
+    if args.varlen:
+        return _varlen_bench(dev, args.steps, args.warmup)
+    if args.decode:
+        return _decode_bench(dev, args.steps, args.warmup)
     if args.model:
         return _model_bench(dev, min(args.steps, 20), min(max(args.warmup, 3), 5),
                             args.model_batch)

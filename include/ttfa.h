@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TTFA_ABI_VERSION 3
+#define TTFA_ABI_VERSION 4
 
 enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
 
@@ -48,6 +48,7 @@ enum ttfa_status {
   TTFA_E_DTYPE = -6,       /* dtype is not a ttfa_dtype                          */
   TTFA_E_SCALE = -7,       /* scale is not finite and positive                   */
   TTFA_E_EPS = -8,         /* eps is not in [0, 1)                               */
+  TTFA_E_QROWS = -9,       /* decode: (Hq / Hkv) * Tq > 32                       */
 };
 
 /* Library ABI version (TTFA_ABI_VERSION of the build). No reference counterpart. */
@@ -127,6 +128,32 @@ int ttfa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
                     const void *dout, const float *lse, float *delta_ws, void *dq, void *dk,
                     void *dv, const int *cu_seqlens, int n_seq, int total, int max_seqlen,
                     int Hq, int Hkv, int D, int dtype, float scale, void *hip_stream);
+
+/*
+ * KV-cache decode attention, bf16 only: Tq new query rows per (batch, query head)
+ * against the first cache_seqlens[b] keys of a [B, Hkv, max_seqlen, D] cache.  Query
+ * row i of batch b sits at position cache_seqlens[b] - Tq + i and sees cache keys
+ * 0 .. cache_seqlens[b] - Tq + i (the new tokens' K/V are already in the cache): the
+ * last Tq rows of the reference's causal attention (model.py:94-98).  No reference
+ * kernel exists (generate.py:7-20 recomputes the prefix; README.md:158 plans a KV
+ * cache).
+ *
+ *   q, o              : [B, Hq, Tq, D] bf16 contiguous
+ *   k_cache, v_cache  : [B, Hkv, max_seqlen, D] bf16 contiguous
+ *   cache_seqlens     : [B] int32 in device memory, 4-byte aligned; values are clamped
+ *                       to 0 .. max_seqlen; a row that sees no key gets O = 0, LSE = -inf
+ *   lse               : [B, Hq, Tq] fp32 out (natural log)
+ *   workspace         : ttfa_decode_workspace_bytes(...) bytes, 16-byte aligned (fp32
+ *                       per-split partials; overwritten)
+ * Supported: D in {64, 128}, Hq % Hkv == 0, (Hq / Hkv) * Tq <= 32 (TTFA_E_QROWS),
+ * B, Tq, max_seqlen >= 1.  Two launches on hip_stream (split pass, merge pass).
+ */
+long long ttfa_decode_workspace_bytes(int B, int Hq, int Hkv, int Tq, int max_seqlen, int D);
+
+int ttfa_decode_fwd(const void *q, const void *k_cache, const void *v_cache,
+                    const int *cache_seqlens, void *o, float *lse, float *workspace, int B,
+                    int Hq, int Hkv, int Tq, int max_seqlen, int D, int dtype, float scale,
+                    void *hip_stream);
 
 /*
  * Fused attention prologue (bf16 only): q/k RMSNorm + rotate-half RoPE + the layout

@@ -231,6 +231,38 @@ def varlen_reference(q: Tensor, k: Tensor, v: Tensor, do: Tensor, cu_seqlens,
     return tuple(outs)
 
 
+def decode_reference(q: Tensor, k_cache: Tensor, v_cache: Tensor, cache_seqlens,
+                     dtype: torch.dtype = torch.float64):
+    """KV-cache decode: q [B, Hq, Tq, D] are the newest Tq query rows of each sequence,
+    row i at position L_b - Tq + i (L_b = cache_seqlens[b] clamped to the cache length)
+    attending causally to cache keys 0 .. L_b - Tq + i -- the last Tq rows of the
+    reference's causal attention (model.py:94-98).  Returns (O [B, Hq, Tq, D],
+    LSE [B, Hq, Tq]); a row that sees no key gets O = 0, LSE = -inf.  Pinned in
+    tests/test_oracle.py against the last rows of ``attention_fwd`` on full sequences."""
+    B, Hq, Tq, D = q.shape
+    Hkv, Lmax = k_cache.shape[1], k_cache.shape[2]
+    G = Hq // Hkv
+    o = torch.zeros((B, Hq, Tq, D), dtype=dtype)
+    lse = torch.full((B, Hq, Tq), float("-inf"), dtype=dtype)
+    for b in range(B):
+        L = min(max(int(cache_seqlens[b]), 0), Lmax)
+        if L == 0:
+            continue
+        k = k_cache[b, :, :L].to(dtype).repeat_interleave(G, 0)
+        v = v_cache[b, :, :L].to(dtype).repeat_interleave(G, 0)
+        s = q[b].to(dtype) @ k.transpose(-1, -2) / math.sqrt(D)
+        pos = torch.arange(Tq)[:, None] + (L - Tq)
+        s = s.masked_fill(torch.arange(L)[None, :] > pos, float("-inf"))
+        seen = pos[:, 0] >= 0
+        if not bool(seen.any()):
+            continue
+        lse_b = torch.logsumexp(s, -1)
+        p = torch.exp(s - lse_b[..., None])
+        o[b][:, seen] = (p @ v)[:, seen]
+        lse[b][:, seen] = lse_b[:, seen]
+    return o, lse
+
+
 def max_abs(a: Tensor, b: Tensor) -> float:
     """max |a - b| in fp64 (NaN anywhere counts as infinite error)."""
     d = (a.detach().double().cpu() - b.detach().double().cpu()).abs()

@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
 
 
 @needs_lib
-@pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7, -8])
+@pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7, -8, -9])
 def test_strerror_names_validation_codes(code):
     msg = _lib.strerror(code)
     assert msg.startswith("ttfa:") and "unknown" not in msg
@@ -303,3 +303,61 @@ def test_varlen_fake_shapes():
         assert o.shape == q.shape and M.shape == (8, 1000) and M.dtype == torch.float32
         dq, dk, dv = torch.ops.tinytrain.flash_attn_varlen_bwd(q, k, k, o, o, M, cu, 512)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+
+
+# ------------------------------------------------------------------ decode entry points
+DC = dict(B=2, Hq=8, Hkv=2, Tq=1, L=1024, D=128, dtype=_lib.TTFA_BF16, scale=0.0884)
+
+
+def _dec(ptrs=None, lens=CU, **kw):
+    a = {**DC, **kw}
+    p = list(P[:3]) + [lens] + list(P[3:6]) if ptrs is None else ptrs
+    return _lib.load().ttfa_decode_fwd(*p, a["B"], a["Hq"], a["Hkv"], a["Tq"], a["L"], a["D"],
+                                       a["dtype"], a["scale"], None)
+
+
+@needs_lib
+@pytest.mark.parametrize("kw,code", [
+    (dict(dtype=_lib.TTFA_F32), _lib.E_DTYPE), (dict(D=80), _lib.E_HEAD_DIM),
+    (dict(Hq=7), _lib.E_GROUP), (dict(B=0), _lib.E_SEQ), (dict(Tq=0), _lib.E_SEQ),
+    (dict(L=0), _lib.E_SEQ), (dict(Tq=9), _lib.E_QROWS), (dict(scale=-1.0), _lib.E_SCALE),
+])
+def test_decode_abi_validation(kw, code):
+    assert _dec(**kw) == code
+
+
+@needs_lib
+def test_decode_abi_pointers_and_workspace():
+    assert _dec(lens=None) == _lib.E_NULL
+    assert _dec(lens=CU + 1) == _lib.E_ALIGN
+    for i in (0, 1, 2, 4, 5, 6):
+        p = list(P[:3]) + [CU] + list(P[3:6])
+        p[i] = None
+        assert _dec(p) == _lib.E_NULL
+    lib = _lib.load()
+    n = lib.ttfa_decode_workspace_bytes(2, 8, 2, 1, 1024, 128)
+    assert n > 0 and n % (4 * (128 + 2)) == 0
+    assert lib.ttfa_decode_workspace_bytes(2, 8, 2, 9, 1024, 128) == -1
+    assert _lib.strerror(_lib.E_QROWS).startswith("ttfa:")
+
+
+def test_decode_input_errors_and_fake():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from tinytrain_amd.kernels.decode import flash_attn_decode
+
+    q = torch.zeros(2, 8, 1, 64, dtype=torch.bfloat16)
+    kc = torch.zeros(2, 2, 100, 64, dtype=torch.bfloat16)
+    lens = torch.tensor([100, 50], dtype=torch.int32)
+    with pytest.raises(fa.FlashAttnInputError, match="32 query rows"):
+        flash_attn_decode(torch.zeros(2, 8, 9, 64, dtype=torch.bfloat16), kc, kc, lens)
+    with pytest.raises(fa.FlashAttnInputError, match="int32"):
+        flash_attn_decode(q, kc, kc, lens.long())
+    with pytest.raises(fa.FlashAttnInputError, match="ROCm GPU"):
+        flash_attn_decode(q, kc, kc, lens)
+    with FakeTensorMode():
+        qf = torch.empty(2, 8, 1, 64, dtype=torch.bfloat16)
+        kf = torch.empty(2, 2, 100, 64, dtype=torch.bfloat16)
+        lf = torch.empty(2, dtype=torch.int32)
+        o, lse = torch.ops.tinytrain.flash_attn_decode(qf, kf, kf, lf)
+        assert o.shape == qf.shape and lse.shape == (2, 8, 1) and lse.dtype == torch.float32

@@ -259,3 +259,33 @@ def test_planted_mask_leak_across_sequences_is_caught():
     leak, _ = attention_fwd(q[None], k[None], v[None])
     assert (o[:, 20:] - leak[0, :, 20:]).abs().max() > 1e-3
     torch.testing.assert_close(o[:, :20], leak[0, :, :20].to(o.dtype), rtol=1e-10, atol=1e-10)
+
+
+def test_decode_reference_is_last_rows_of_causal_attention():
+    """Decode with the cache holding a sequence's K/V equals the last Tq rows of full
+    causal attention over that sequence (per batch, with per-batch lengths)."""
+    from oracle.eager_attention import decode_reference
+
+    g = torch.Generator().manual_seed(5)
+    B, Hq, Hkv, D, Lmax, Tq = 3, 4, 2, 64, 40, 3
+    lens = [40, 17, 3]
+    kc = torch.randn(B, Hkv, Lmax, D, generator=g, dtype=torch.float64)
+    vc = torch.randn(B, Hkv, Lmax, D, generator=g, dtype=torch.float64)
+    qfull = torch.randn(B, Hq, Lmax, D, generator=g, dtype=torch.float64)
+    q = torch.stack([qfull[b, :, lens[b] - Tq:lens[b]] for b in range(B)])
+    o, lse = decode_reference(q, kc, vc, lens)
+    for b in range(B):
+        L = lens[b]
+        of, lf = attention_fwd(qfull[b:b + 1, :, :L], kc[b:b + 1, :, :L], vc[b:b + 1, :, :L])
+        torch.testing.assert_close(o[b], of[0, :, L - Tq:L], rtol=1e-10, atol=1e-10)
+        torch.testing.assert_close(lse[b], lf[0, :, L - Tq:L], rtol=1e-10, atol=1e-10)
+
+
+def test_decode_reference_rows_without_keys():
+    from oracle.eager_attention import decode_reference
+
+    q = torch.randn(1, 2, 4, 64, dtype=torch.float64)
+    kc = torch.randn(1, 1, 8, 64, dtype=torch.float64)
+    o, lse = decode_reference(q, kc, kc, [2])  # rows 0, 1 sit at positions -2, -1
+    assert torch.all(o[0, :, :2] == 0) and torch.all(torch.isinf(lse[0, :, :2]))
+    assert torch.isfinite(lse[0, :, 2:]).all()

@@ -29,6 +29,19 @@ hipError_t launch_bwd_varlen_bf16(const void *q, const void *k, const void *v, c
                                   int total, int max_seqlen, int Hq, int Hkv, int D, float scale,
                                   hipStream_t stream);
 
+// KV-cache decode: q/o [B, Hq, Tq, D], caches [B, Hkv, Lmax, D], lse [B, Hq, Tq],
+// cache_seqlens [B] int32 on the device; workspace of decode_workspace_floats() floats.
+struct DecodeSplit {
+  int wkeys;     // keys per wave (a multiple of 32)
+  int n_chunks;  // workgroups per (batch, KV head)
+  int n_splits;  // partials per query row (4 per workgroup)
+};
+DecodeSplit decode_split(int B, int Hkv, int Lmax);
+hipError_t launch_decode_bf16(const void *q, const void *k_cache, const void *v_cache,
+                              const int *cache_seqlens, void *o, float *lse, float *workspace,
+                              int B, int Hq, int Hkv, int Tq, int Lmax, int D, float scale,
+                              hipStream_t stream);
+
 hipError_t launch_fwd_f32(const void *q, const void *k, const void *v, void *o, float *lse,
                           int B, int Hq, int Hkv, int T, int D, float scale, hipStream_t stream);
 hipError_t launch_bwd_dq_f32(const void *q, const void *k, const void *v, const void *o,

@@ -41,6 +41,20 @@ int check_varlen(int n_seq, int total, int max_seqlen, int Hq, int Hkv, int D, i
   return TTFA_OK;
 }
 
+// KV-cache decode: bf16; G * Tq query columns fit one 32-wide MFMA tile; cache byte
+// extents within the 32-bit buffer descriptors.
+int check_decode(int B, int Hq, int Hkv, int Tq, int Lmax, int D, int dtype, float scale) {
+  if (dtype != TTFA_BF16) return TTFA_E_DTYPE;
+  if (D != 64 && D != 128) return TTFA_E_HEAD_DIM;
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0) return TTFA_E_GROUP;
+  if (B < 1 || Tq < 1 || Lmax < 1) return TTFA_E_SEQ;
+  if ((int64_t)(Hq / Hkv) * Tq > 32) return TTFA_E_QROWS;
+  if ((int64_t)Lmax * D * 2 > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  if ((int64_t)B * Hq * Tq > (int64_t)0x7fffffff / 4) return TTFA_E_SEQ;
+  if (!(scale > 0.f) || !isfinite(scale)) return TTFA_E_SCALE;
+  return TTFA_OK;
+}
+
 int check_ptrs(const void *const *ptrs, int n) {
   for (int i = 0; i < n; ++i)
     if (ptrs[i] == nullptr) return TTFA_E_NULL;
@@ -66,6 +80,7 @@ const char *ttfa_strerror(int code) {
     case TTFA_E_DTYPE: return "ttfa: dtype must be TTFA_BF16 or TTFA_F32";
     case TTFA_E_SCALE: return "ttfa: scale must be finite and > 0";
     case TTFA_E_EPS: return "ttfa: eps must be in [0, 1)";
+    case TTFA_E_QROWS: return "ttfa: decode needs (Hq / Hkv) * Tq <= 32 query rows per KV head";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -142,6 +157,27 @@ int ttfa_varlen_bwd(const void *q, const void *k, const void *v, const void *o,
   return static_cast<int>(ttfa::launch_bwd_varlen_bf16(
       q, k, v, o, dout, lse, delta_ws, dq, dk, dv, cu_seqlens, n_seq, total, max_seqlen, Hq, Hkv,
       D, scale, static_cast<hipStream_t>(hip_stream)));
+}
+
+long long ttfa_decode_workspace_bytes(int B, int Hq, int Hkv, int Tq, int max_seqlen, int D) {
+  if (check_decode(B, Hq, Hkv, Tq, max_seqlen, D, TTFA_BF16, 1.f)) return -1;
+  const ttfa::DecodeSplit sp = ttfa::decode_split(B, Hkv, max_seqlen);
+  return (long long)B * Hq * Tq * sp.n_splits * (D + 2) * (long long)sizeof(float);
+}
+
+int ttfa_decode_fwd(const void *q, const void *k_cache, const void *v_cache,
+                    const int *cache_seqlens, void *o, float *lse, float *workspace, int B,
+                    int Hq, int Hkv, int Tq, int max_seqlen, int D, int dtype, float scale,
+                    void *hip_stream) {
+  int rc = check_decode(B, Hq, Hkv, Tq, max_seqlen, D, dtype, scale);
+  if (rc) return rc;
+  const void *ptrs[] = {q, k_cache, v_cache, o, lse, workspace};
+  if ((rc = check_ptrs(ptrs, 6))) return rc;
+  if (cache_seqlens == nullptr) return TTFA_E_NULL;
+  if (reinterpret_cast<uintptr_t>(cache_seqlens) & 3u) return TTFA_E_ALIGN;
+  return static_cast<int>(ttfa::launch_decode_bf16(q, k_cache, v_cache, cache_seqlens, o, lse,
+                                                   workspace, B, Hq, Hkv, Tq, max_seqlen, D,
+                                                   scale, static_cast<hipStream_t>(hip_stream)));
 }
 
 int ttfa_bwd(const void *q, const void *k, const void *v, const void *o, const void *dout,
