@@ -213,51 +213,65 @@ __global__ __launch_bounds__(256, 2) void fa_decode_bf16_kernel(
 
 // Merge the n_splits partials of every query row: M = max m over partials with l > 0,
 // O = sum o_s 2^(m_s - M) / sum l_s 2^(m_s - M), LSE = (M + log2 sum) ln 2; a row with no
-// visible key gets O = 0, LSE = -inf.  One wave per row: the lanes split the partials for
-// M and the weights (kept in LDS), then each lane sums D/64 columns over all partials in
-// index order (independent loads, unrolled).
+// visible key gets O = 0, LSE = -inf.  One 256-thread workgroup per row: the threads
+// split the partials for M and the weights (kept in LDS); then thread t sums float4
+// column t % (D/4) over the partials s = t / (D/4) (mod 256 / (D/4)), loads issued
+// unconditionally (a partial without keys holds zeros and weight 0), and the groups are
+// added in a fixed order, so the result does not depend on timing.
 template <int D>
 __global__ __launch_bounds__(256) void fa_decode_combine_kernel(
     const float *__restrict__ part_o, const float *__restrict__ part_ml, bf16 *__restrict__ O,
     float *__restrict__ LSE, int rows, int n_splits) {
-  constexpr int E = D / 64;
-  __shared__ float wts[4][kDecMaxSplits];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + wave;
-  if (row >= rows) return;  // whole waves leave; no workgroup barrier below
+  constexpr int C4 = D / 4, SG = 256 / C4;
+  __shared__ float wts[kDecMaxSplits];
+  __shared__ float red[8];
+  __shared__ f32x4 accs[SG][C4];
+  const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float *ml = part_ml + (int64_t)row * n_splits * 2;
   float M = -INFINITY;
-  for (int s = lane; s < n_splits; s += 64)
-    if (ml[2 * s + 1] > 0.f) M = fmax2(M, ml[2 * s]);
+  for (int s = tid; s < n_splits; s += 256) {
+    const f32x2 v = *reinterpret_cast<const f32x2 *>(ml + 2 * s);
+    if (v[1] > 0.f) M = fmax2(M, v[0]);
+  }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) M = fmax2(M, __shfl_xor(M, m));
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = fmax2(fmax2(red[0], red[1]), fmax2(red[2], red[3]));
   float lsum = 0.f;
-  for (int s = lane; s < n_splits; s += 64) {
-    const float ls = ml[2 * s + 1];
-    const float w = (ls > 0.f && M != -INFINITY) ? exp2f_fast(ml[2 * s] - M) : 0.f;
-    wts[wave][s] = w;
-    lsum = __builtin_fmaf(ls > 0.f ? ls : 0.f, w, lsum);
+  for (int s = tid; s < n_splits; s += 256) {
+    const f32x2 v = *reinterpret_cast<const f32x2 *>(ml + 2 * s);
+    const float w = (v[1] > 0.f && M != -INFINITY) ? exp2f_fast(v[0] - M) : 0.f;
+    wts[s] = w;
+    lsum = __builtin_fmaf(v[1] > 0.f ? v[1] : 0.f, w, lsum);
   }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) lsum += __shfl_xor(lsum, m);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done (lgkmcnt(0))
-  __builtin_amdgcn_wave_barrier();
-  float acc[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  const float *po = part_o + (int64_t)row * n_splits * D + lane * E;
+  if (lane == 0) red[4 + wave] = lsum;
+  __syncthreads();  // wts and the sums are visible
+  lsum = (red[4] + red[5]) + (red[6] + red[7]);
+  const int c = tid % C4, sg = tid / C4;
+  const f32x4 *po = reinterpret_cast<const f32x4 *>(part_o + (int64_t)row * n_splits * D) + c;
+  f32x4 acc{};
 #pragma unroll 4
-  for (int s = 0; s < n_splits; ++s) {
-    const float w = wts[wave][s];  // wave-uniform: partials without keys are skipped
-    if (w != 0.f) {
+  for (int s = sg; s < n_splits; s += SG) {
+    const f32x4 x = po[(int64_t)s * C4];
+    const float w = wts[s];
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(po[(int64_t)s * D + e], w, acc[e]);
-    }
+    for (int e = 0; e < 4; ++e) acc[e] = w != 0.f ? __builtin_fmaf(x[e], w, acc[e]) : acc[e];
   }
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  accs[sg][c] = acc;
+  __syncthreads();
+  if (tid < C4) {
+    f32x4 t = accs[0][tid];
 #pragma unroll
-  for (int e = 0; e < E; ++e) O[(int64_t)row * D + lane * E + e] = (bf16)(acc[e] * inv);
-  if (lane == 0) LSE[row] = lsum > 0.f ? (M + __log2f(lsum)) * kLn2 : -INFINITY;
+    for (int g = 1; g < SG; ++g) t += accs[g][tid];
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    bf16 *out = O + (int64_t)row * D + 4 * tid;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = (bf16)(t[e] * inv);
+  }
+  if (tid == 0) LSE[row] = lsum > 0.f ? (M + __log2f(lsum)) * kLn2 : -INFINITY;
 }
 
 // Keys per wave: enough waves to fill the device (about 2048), at least 128 keys per
@@ -291,7 +305,7 @@ hipError_t launch_decode_bf16(const void *q, const void *k_cache, const void *v_
   float *part_ml = workspace + (int64_t)rows * sp.n_splits * D;
   const float sl2 = scale * kLog2e;
   const dim3 grid((unsigned)((int64_t)B * Hkv * sp.n_chunks)), block(256);
-  const dim3 cgrid((unsigned)((rows + 3) / 4)), cblock(256);
+  const dim3 cgrid((unsigned)rows), cblock(256);
   if (D == 64) {
     fa_decode_bf16_kernel<64><<<grid, block, 0, stream>>>(
         (const bf16 *)q, (const bf16 *)k_cache, (const bf16 *)v_cache, cache_seqlens, part_o,
