@@ -307,13 +307,17 @@ inline bool use_pairs(int n_tiles, int B, int H, int slots) {
 // left the higher priority (0..3, by quarters of its total) keeps them in step, so the
 // CU stays fully occupied until all of them finish.
 struct PrioByRemaining {
-  int total, lvl = -1;
+  int total, lvl = -1, floor_r = 0;  // the level holds while remaining >= floor_r
   __device__ explicit PrioByRemaining(int total_) : total(total_ > 0 ? total_ : 1) {}
   // remaining >= total * k/4 for k = 1, 2, 3 gives level k; s_setprio runs only when the
-  // level changes (its operand is an immediate, hence the branches).
+  // level changes (its operand is an immediate, hence the branches).  Remaining work only
+  // decreases, so the common case is one scalar compare against the current level's
+  // floor.
   __device__ __forceinline__ void update(int remaining) {
+    if (lvl >= 0 && remaining >= floor_r) return;
     const int r4 = 4 * remaining;
-    const int l = (r4 >= total) + (r4 >= 2 * total) + (r4 >= 3 * total);
+    const int l = r4 >= 3 * total ? 3 : r4 >= 2 * total ? 2 : r4 >= total ? 1 : 0;
+    floor_r = (l * total + 3) / 4;  // smallest remaining with 4 * remaining >= l * total
     if (l == lvl) return;
     lvl = l;
     if (l == 3)

@@ -67,13 +67,32 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
     for (int kk = 1; kk < P::KK; ++kk) s[kb] = mfma32(kf[kb][kk], qf[kk], s[kb]);
   }
   if (MASK) {
+    if (k0 + P::BN <= T) {
+      // Inside T, every 32-key block is either visible, entirely above the wave's 32 rows,
+      // or exactly on their diagonal (rows and blocks both start at multiples of 32);
+      // which one is wave-uniform, and the diagonal pattern is key slot > row.
+      const int q0 = qrow - lq, dl = lq - 4 * lg;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb) {
+        const int rel = k0 + 32 * kb - q0;
+        if (rel > 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (key > qrow || key >= T) s[kb][r] = -INFINITY;
+          for (int r = 0; r < 16; ++r) s[kb][r] = -INFINITY;
+        } else if (rel == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) > dl) s[kb][r] = -INFINITY;
+        }
       }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+          if (key > qrow || key >= T) s[kb][r] = -INFINITY;
+        }
+    }
   }
   // Row max of this tile (v_max3 tree), then the lazy running-max update.
   float mx = max16(s[1], max16(s[0], -INFINITY));
@@ -88,14 +107,21 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
   }
   // P = exp2(S * scale*log2e - m) in fp32 (row sum), packed to bf16 for the PV product.
   bf16x8 pb[4];
-  float rs0 = 0.f, rs1 = 0.f;
+  float rs0, rs1;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     float p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) p[e] = exp2f_fast(__builtin_fmaf(s[m >> 1][8 * (m & 1) + e], scale_log2, -m_t));
+    if (m == 0) {  // the sums start at the first terms (0 + x is not folded: -0)
+      rs0 = p[0];
+      rs1 = p[1];
+    } else {
+      rs0 += p[0];
+      rs1 += p[1];
+    }
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
+    for (int e = 2; e < 8; e += 2) {
       rs0 += p[e];
       rs1 += p[e + 1];
     }
@@ -144,15 +170,26 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
 
   // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
   // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
-  // holds logical chunk phys ^ swizzle(row).
+  // holds logical chunk phys ^ swizzle(row).  The lane's offset within a tile is fixed
+  // (voffset); the tile's start is the scalar soffset; the LDS destination (M0) comes
+  // from the scalar wave index.
+  const int wave_s = wave_id();
+  uint32_t voff[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int e = 256 * i + 64 * wave + lane, row = e / CH, pc = e % CH;
+    voff[i] = (uint32_t)(row * D + swz<D>(row, pc) * 8) * 2;
+  }
   auto load_tile = [&](int j, int stage) {
+    // descriptors re-based at the tile (scalar work): rows past T still read as zero
+    const int64_t t0 = (int64_t)j * BN * D;
+    const uint32_t left = head_bytes - (uint32_t)t0 * 2;
+    const auto rkj = make_rsrc(hd.k + t0, left), rvj = make_rsrc(hd.v + t0, left);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
-      const int lc = swz<D>(row, pc);
-      const uint32_t off = (uint32_t)((j * BN + row) * D + lc * 8) * 2;
-      buf_load16_lds(rk, off, &lds[stage][0][e0 * 8]);
-      buf_load16_lds(rv, off, &lds[stage][1][e0 * 8]);
+      const int e0 = 256 * i + 64 * wave_s;
+      buf_load16_lds(rkj, voff[i], &lds[stage][0][e0 * 8]);
+      buf_load16_lds(rvj, voff[i], &lds[stage][1][e0 * 8]);
     }
   };
 
