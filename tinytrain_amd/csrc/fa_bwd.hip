@@ -83,17 +83,39 @@ __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf
       dp[kb] = mfma32(vf[kk], dof[kk], dp[kb]);
     }
   }
+  if (MASK) {
+    if (k0 + P::BN <= T) {
+      // Inside T, every 32-key block is visible, entirely above the wave's 32 rows, or
+      // exactly on their diagonal (rows and blocks start at multiples of 32), which is
+      // wave-uniform; on the diagonal a slot is masked when its key slot exceeds the row.
+      const int dl = lq - 4 * lg;
+#pragma unroll
+      for (int kb = 0; kb < P::KB; ++kb) {
+        const int rel = k0 + 32 * kb - (qrow - lq);
+        if (rel > 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[kb][r] = -INFINITY;
+        } else if (rel == 0) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) > dl) s[kb][r] = -INFINITY;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < P::KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
+          if (key > qrow || key >= T) s[kb][r] = -INFINITY;
+        }
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float x = __builtin_fmaf(s[kb][r], scale_log2, -lse_t);
-      if (MASK) {
-        const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (key > qrow || key >= T) x = -INFINITY;
-      }
-      s[kb][r] = exp2f_fast(x) * dp[kb][r];  // dS^T = P^T (dP^T - Delta)
-    }
+    for (int r = 0; r < 16; ++r)  // dS^T = P^T (dP^T - Delta); -inf scores give P = 0
+      s[kb][r] = exp2f_fast(__builtin_fmaf(s[kb][r], scale_log2, -lse_t)) * dp[kb][r];
 #pragma unroll
   for (int m = 0; m < P::BN / 16; ++m) {
     const bf16x8 dsb = pack8(s[m >> 1], 8 * (m & 1));
@@ -213,19 +235,29 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   const auto rq = make_rsrc(hd.q, head_bytes);
   const auto ro = make_rsrc(hd.o, head_bytes);
   const auto rdo = make_rsrc(hd.dout, head_bytes);
-  const auto rk = make_rsrc(hd.k, head_bytes);
-  const auto rv = make_rsrc(hd.v, head_bytes);
 
   // Global -> LDS without registers: lane l of the wave's 1 KB block e0 writes physical
   // chunk (e0 + l) % CH of row (e0 + l) / CH, which holds logical chunk phys ^ swizzle(row).
+  // The lane's offset within a tile is fixed; the descriptors are re-based at the tile
+  // (scalar work; rows past T still read as zero) and the LDS destinations (M0) come
+  // from the scalar wave index.
+  const int wave_s = wave_id();
+  uint32_t voff[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int e = 256 * i + 64 * wave + lane, row = e / CH, pc = e % CH;
+    voff[i] = (uint32_t)(row * D + swz<D>(row, pc) * 8) * 2;
+  }
   auto load_tile = [&](int j, int stage) {
     bf16 *Kt = lds + stage * 2 * BN * D, *Vt = Kt + BN * D;
+    const int64_t t0 = (int64_t)j * BN * D;
+    const uint32_t left = head_bytes - (uint32_t)t0 * 2;
+    const auto rkj = make_rsrc(hd.k + t0, left), rvj = make_rsrc(hd.v + t0, left);
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-      const int e0 = 256 * i + 64 * wave, e = e0 + lane, row = e / CH, pc = e % CH;
-      const uint32_t off = (uint32_t)((j * BN + row) * D + swz<D>(row, pc) * 8) * 2;
-      buf_load16_lds(rk, off, Kt + e0 * 8);
-      buf_load16_lds(rv, off, Vt + e0 * 8);
+      const int e0 = 256 * i + 64 * wave_s;
+      buf_load16_lds(rkj, voff[i], Kt + e0 * 8);
+      buf_load16_lds(rvj, voff[i], Vt + e0 * 8);
     }
   };
 
