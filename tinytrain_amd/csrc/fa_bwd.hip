@@ -58,7 +58,7 @@ struct DkvTile {
   static constexpr int LDS_BYTES = 2 * 2 * BMQ * D * 2 + 2 * 2 * BMQ * 4;
 };
 
-// One key tile of the dQ pass for one wave.
+// One key tile of the dQ pass for one wave, one 32-key block at a time.
 template <int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf16x8 (&qf)[D / 16],
                                         const bf16x8 (&dof)[D / 16], const f32x16 &ndelta,
@@ -66,64 +66,56 @@ __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf
                                         int k0, int qrow, int T, int lane) {
   using P = DqTile<D>;
   const int lq = lane & 31, lg = lane >> 5;
-  f32x16 s[P::KB], dp[P::KB];
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb) {
-    bf16x8 kf[P::KK], vf[P::KK];
+    f32x16 s, dp;
+    {
+      bf16x8 kf[P::KK], vf[P::KK];
 #pragma unroll
-    for (int kk = 0; kk < P::KK; ++kk) {
-      kf[kk] = lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg);
-      vf[kk] = lds_read_row8<D>(Vt, kb * 32 + lq, 2 * kk + lg);
+      for (int kk = 0; kk < P::KK; ++kk) {
+        kf[kk] = lds_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg);
+        vf[kk] = lds_read_row8<D>(Vt, kb * 32 + lq, 2 * kk + lg);
+      }
+      s = mfma32(kf[0], qf[0], f32x16{});
+      dp = mfma32(vf[0], dof[0], ndelta);
+#pragma unroll
+      for (int kk = 1; kk < P::KK; ++kk) {
+        s = mfma32(kf[kk], qf[kk], s);
+        dp = mfma32(vf[kk], dof[kk], dp);
+      }
     }
-    s[kb] = mfma32(kf[0], qf[0], f32x16{});
-    dp[kb] = mfma32(vf[0], dof[0], ndelta);
-#pragma unroll
-    for (int kk = 1; kk < P::KK; ++kk) {
-      s[kb] = mfma32(kf[kk], qf[kk], s[kb]);
-      dp[kb] = mfma32(vf[kk], dof[kk], dp[kb]);
-    }
-  }
-  if (MASK) {
-    if (k0 + P::BN <= T) {
-      // Inside T, every 32-key block is visible, entirely above the wave's 32 rows, or
-      // exactly on their diagonal (rows and blocks start at multiples of 32), which is
-      // wave-uniform; on the diagonal a slot is masked when its key slot exceeds the row.
-      const int dl = lq - 4 * lg;
-#pragma unroll
-      for (int kb = 0; kb < P::KB; ++kb) {
-        const int rel = k0 + 32 * kb - (qrow - lq);
+    if (MASK) {
+      const int kbase = k0 + 32 * kb;
+      if (k0 + P::BN <= T) {
+        const int rel = kbase - (qrow - lq), dl = lq - 4 * lg;
         if (rel > 0) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[kb][r] = -INFINITY;
+          for (int r = 0; r < 16; ++r) s[r] = -INFINITY;
         } else if (rel == 0) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (8 * (r >> 2) + (r & 3) > dl) s[kb][r] = -INFINITY;
+            if (8 * (r >> 2) + (r & 3) > dl) s[r] = -INFINITY;
         }
-      }
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < P::KB; ++kb)
+      } else {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = k0 + kb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-          if (key > qrow || key >= T) s[kb][r] = -INFINITY;
+          const int key = kbase + 8 * (r >> 2) + 4 * lg + (r & 3);
+          if (key > qrow || key >= T) s[r] = -INFINITY;
         }
+      }
     }
-  }
-#pragma unroll
-  for (int kb = 0; kb < P::KB; ++kb)
 #pragma unroll
     for (int r = 0; r < 16; ++r)  // dS^T = P^T (dP^T - Delta); -inf scores give P = 0
-      s[kb][r] = exp2f_fast(__builtin_fmaf(s[kb][r], scale_log2, -lse_t)) * dp[kb][r];
+      s[r] = exp2f_fast(__builtin_fmaf(s[r], scale_log2, -lse_t)) * dp[r];
 #pragma unroll
-  for (int m = 0; m < P::BN / 16; ++m) {
-    const bf16x8 dsb = pack8(s[m >> 1], 8 * (m & 1));
-    bf16x8 kt[P::DB];
+    for (int m = 0; m < 2; ++m) {
+      const bf16x8 dsb = pack8(s, 8 * m);
+      bf16x8 kt[P::DB];
 #pragma unroll
-    for (int db = 0; db < P::DB; ++db) kt[db] = lds_read_trT<D>(Kt, 16 * m, 32 * db, lane);
+      for (int db = 0; db < P::DB; ++db) kt[db] = lds_read_trT<D>(Kt, 32 * kb + 16 * m, 32 * db, lane);
 #pragma unroll
-    for (int db = 0; db < P::DB; ++db) dqacc[db] = mfma32(kt[db], dsb, dqacc[db]);
+      for (int db = 0; db < P::DB; ++db) dqacc[db] = mfma32(kt[db], dsb, dqacc[db]);
+    }
   }
 }
 
@@ -226,7 +218,12 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   const int T = hd.T;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // An opaque copy of the thread id: the batched kernel inlines this body twice (paired
+  // row tiles), and without it the compiler shares lane-derived addresses between the
+  // two copies, which keeps them live across the first.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 31, lg = lane >> 5;
   const int q0 = qt * BM + wave * 32;
   const int qrow = q0 + lq;
@@ -313,7 +310,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
 }
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
+// D = 64: three workgroups per CU (at most 168 VGPRs; a few values of the second row
+// tile spill, which measured faster than two workgroups without spills).
+__global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
@@ -342,7 +341,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq_bf16_kernel(
 // sequence, query head), rank-major, longest row tiles first; invalid sequence bounds
 // are skipped.
 template <int D>
-__global__ __launch_bounds__(256, 2) void fa_bwd_dq_varlen_bf16_kernel(
+__global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, const int *__restrict__ cu_seqlens,
