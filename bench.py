@@ -118,11 +118,12 @@ def _gemm_reference(dev, n: int = 8192, steps: int = 30) -> dict:
     for _ in range(5):
         torch.matmul(a, b)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    stream = torch.cuda.current_stream(dev)
+    evs = [(HipTimingEvent(), HipTimingEvent()) for _ in range(steps)]
     for e0, e1 in evs:
-        e0.record()
+        e0.record(stream)
         torch.matmul(a, b)
-        e1.record()
+        e1.record(stream)
     torch.cuda.synchronize()
     ms = statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
     return {"shape": [n, n, n], "library": "torch.matmul (hipBLASLt), bf16 in, fp32 accumulate",
@@ -321,19 +322,68 @@ def _copy_probe(mb: float, steps: int, dev) -> int:
     return 0
 
 
+class HipTimingEvent:
+    """A HIP event for timing only, recorded on a given stream: created with
+    hipEventDisableSystemFence, so its completion carries no system-scope release.  On
+    MI355X a default event (torch.cuda.Event) recorded between two launches adds a few
+    microseconds to their span; this one adds about half of that.  Same record /
+    elapsed_time interface as torch.cuda.Event."""
+
+    _hip = None
+    FLAGS = 0x20000000  # hipEventDisableSystemFence (hip_runtime_api.h)
+
+    @classmethod
+    def _lib(cls):
+        if cls._hip is None:
+            import ctypes
+
+            h = ctypes.CDLL("libamdhip64.so")
+            h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                              ctypes.c_void_p]
+            h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+
+        self._e = ctypes.c_void_p()
+        if self._lib().hipEventCreateWithFlags(ctypes.byref(self._e), self.FLAGS) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+
+    def record(self, stream):
+        if self._lib().hipEventRecord(self._e, stream.cuda_stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_time(self, other) -> float:
+        import ctypes
+
+        ms = ctypes.c_float()
+        if self._lib().hipEventElapsedTime(ctypes.byref(ms), self._e, other._e) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        if self._e and self._hip is not None:
+            self._hip.hipEventDestroy(self._e)
+
+
 def _ev_time(fn, steps: int, warmup: int) -> float:
-    """Median ms of ``fn`` over ``steps`` calls (HIP events on the current stream)."""
+    """Median ms of ``fn`` over ``steps`` calls (timing-only HIP events on the current
+    stream around each call)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    stream = torch.cuda.current_stream()
+    evs = [(HipTimingEvent(), HipTimingEvent()) for _ in range(steps)]
     for e0, e1 in evs:
-        e0.record()
+        e0.record(stream)
         fn()
-        e1.record()
+        e1.record(stream)
     torch.cuda.synchronize()
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
 
@@ -727,18 +777,27 @@ def main() -> int:
         launch(sets[i % nsets])
     torch.cuda.synchronize()
 
+    # Timed region: K steps back to back, bracketed by events after a synchronize; no
+    # event between the launches (one recorded between two kernels lengthens the step).
     K = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(K):
-        launch(sets[i % nsets], evs[i])
+        launch(sets[i % nsets])
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = start.elapsed_time(end) / K
+
+    # Per-kernel breakdown: K more steps on the same rotation, with timing-only HIP events
+    # on the launch stream between the three launches of every step.
+    evs = [[HipTimingEvent() for _ in range(4)] for _ in range(K)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        launch(sets[i % nsets], evs[i])
+    torch.cuda.synchronize()
 
     def per_kernel(evlist):
         kms = {"fwd": [], "bwd_dq": [], "bwd_dkdv": []}
@@ -755,7 +814,7 @@ def main() -> int:
     # Hot-cache pass (outside the timed region above): the same input set every step, so
     # K/V and Q stay in the Infinity Cache; reported separately.
     Kh = 0 if args.no_extras else min(K, 50)
-    evh = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(Kh)]
+    evh = [[HipTimingEvent() for _ in range(4)] for _ in range(Kh)]
     for i in range(5 if Kh else 0):
         launch(sets[0])
     for i in range(Kh):
@@ -810,6 +869,10 @@ def main() -> int:
             "bwd_dq_ms": round(avg["bwd_dq"], 5),
             "bwd_dkdv_ms": round(avg["bwd_dkdv"], 5),
             "median_ms": {n: round(x, 5) for n, x in med.items()},
+            "timing": "per-kernel times from a second run of K steps right after the timed "
+                      "region, timing-only HIP events (hipEventDisableSystemFence) between "
+                      "the launches on their stream; value and ms_per_step come from the "
+                      "timed region, which records no event between launches",
         },
         "hot_cache": None if hot is None else {
             "note": "same input set every step (working set resident in the 256 MB Infinity "
