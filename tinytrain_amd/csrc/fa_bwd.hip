@@ -300,6 +300,7 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
       dq_tile<D, false>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
       dq_tile<D, true>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
+    wait_vm_all();  // tile j+1 is in LDS before any wave passes the barrier
     __syncthreads();
   }
 
@@ -414,7 +415,11 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
   const int n_items = G * per_g;
 
   const float inv_scale = 1.f / scale;
-  float fl = 0.f;  // one -LSE/scale or -Delta value for threads < 128
+  // Threads < 128 carry one LSE (tid < 64) or Delta value of the next item from its load
+  // to its staging: loaded raw, so nothing waits on the load (nor on the Q/dO tile loads
+  // issued before it) until the value is staged after the current item's compute.
+  float fl = 0.f;
+  const uint32_t row_bytes = (uint32_t)T * 4;  // LSE / Delta rows past T read as zero
   // Items run over the group's query heads g, and for each over the query tiles
   // qt_lo..n_qt-1; (ld_g, ld_qt) is the next item to load.
   int ld_g = 0, ld_qt = qt_lo;
@@ -431,6 +436,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
     const auto rq = make_rsrc(hd.q + g * hd.head_stride, head_bytes);
     const auto rdo = make_rsrc(hd.dout + g * hd.head_stride, head_bytes);
     const float *lse_g = hd.lse + g * hd.row_stride, *delta_g = hd.delta + g * hd.row_stride;
+    const auto rfl = make_rsrc(wave_u == 0 ? lse_g : delta_g, row_bytes);  // wave-uniform
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
@@ -438,14 +444,11 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
       buf_load16_lds(rq, off, Qt + e0 * 8);
       buf_load16_lds(rdo, off, dOt + e0 * 8);
     }
-    if (tid < 2 * BMQ) {
-      const int r = qt * BMQ + (tid & (BMQ - 1));
-      fl = 0.f;
-      if (r < T) fl = tid < BMQ ? -lse_g[r] * inv_scale : -delta_g[r];
-    }
+    if (tid < 2 * BMQ)
+      fl = __uint_as_float(buf_load4(rfl, (uint32_t)(qt * BMQ + (tid & (BMQ - 1))) * 4));
   };
   auto stage_rows = [&](int stage) {
-    if (tid < 2 * BMQ) ldsf[stage * 2 * BMQ + tid] = fl;
+    if (tid < 2 * BMQ) ldsf[stage * 2 * BMQ + tid] = tid < BMQ ? -fl * inv_scale : -fl;
   };
 
   f32x16 dkacc[DB], dvacc[DB];
@@ -489,6 +492,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
       }
     }
     if (it + 1 < n_items) stage_rows((it + 1) & 1);
+    wait_vm_all();  // item it+1's Q/dO tiles are in LDS before any wave passes the barrier
     __syncthreads();
   }
 

@@ -50,6 +50,10 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t b
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0);
 }
 
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
+
 // 16 bytes per lane straight from a buffer into LDS: the wave's 64 lanes fill the
 // 1 KB at lds_wave (wave-uniform) in lane order.
 __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, void *lds_wave) {
@@ -59,6 +63,9 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_
 // Index of the calling wave in its workgroup as a wave-uniform (scalar) value, so LDS
 // addresses derived from it stay in SGPRs (M0 of the LDS-direct loads needs no
 // v_readfirstlane per load).
+// s_waitcnt vmcnt(0): every vector memory load of this wave (direct-to-LDS included) done.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // LDS tiles are row-major [rows][D] bf16, stored in 16-byte chunks whose index is
@@ -101,7 +108,12 @@ __device__ __forceinline__ bf16x8 lds_read_row8(const bf16 *tile, int row, int c
   return *reinterpret_cast<const bf16x8 *>(tile + row * D + (swz<D>(row, chunk) << 3));
 }
 
-__device__ __forceinline__ bf16x4 lds_read_tr(const bf16 *p) {
+// The pointer is __restrict__ so that, once inlined, the read carries alias-scope
+// metadata: without it the compiler makes every transposed read wait (vmcnt) for all
+// direct-to-LDS loads in flight, including the next tile's prefetch into the other LDS
+// stage.  The kernels order each stage's loads before its reads explicitly (vmcnt(0)
+// and a barrier between the two).
+__device__ __forceinline__ bf16x4 lds_read_tr(const bf16 *__restrict__ p) {
   typedef TTFA_LDS bf16x4 lds_bf16x4;
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)(p));
 }

@@ -226,6 +226,7 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
       fwd_tile<D, false>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
       fwd_tile<D, true>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
+    wait_vm_all();  // tile j+1 is in LDS before any wave passes the barrier
     __syncthreads();
   }
 
