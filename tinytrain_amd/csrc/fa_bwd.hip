@@ -218,9 +218,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   const int T = hd.T;
 
-  // An opaque copy of the thread id: the batched kernel inlines this body twice (paired
-  // row tiles), and without it the compiler shares lane-derived addresses between the
-  // two copies, which keeps them live across the first.
+  // An opaque copy of the thread id: the batched kernel at D = 128 inlines this body
+  // twice (paired row tiles), and without it the compiler shares lane-derived addresses
+  // between the two copies, which keeps them live across the first.
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int wave = tid >> 6, lane = tid & 63;
@@ -311,8 +311,7 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
 }
 
 template <int D>
-// D = 64: three workgroups per CU (at most 168 VGPRs; a few values of the second row
-// tile spill, which measured faster than two workgroups without spills).
+// D = 64: three workgroups per CU (at most 168 VGPRs).
 __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
@@ -334,7 +333,10 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_bf16_kernel(
   const DqHead hd{Q + qb, K + kvh * hs, V + kvh * hs, O + qb, dO + qb,
                   LSE + (int64_t)w.bh * T, Delta + (int64_t)w.bh * T, dQ + qb, T};
   dq_rows<D>(smem, hd, w.first, scale_log2, scale, w1 + w2, wmax);
-  if (w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
+  // D = 64 runs single tiles only (the launcher never pairs it): a second inlined copy of
+  // the row body would not fit three workgroups per CU without spills, and the spill
+  // reloads wait on the tile prefetch.  Longest-first singles balance as well here.
+  if (D != 64 && w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
 }
 
 // Packed variable-length sequences ([H, total, D], sequence s at rows cu_seqlens[s] ..
@@ -577,7 +579,8 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
     hipError_t e = allow_lds(kern, lds);
     if (e != hipSuccess) return e;
   }
-  const bool paired = use_pairs(n_tiles, B, Hq, resident_slots<fa_bwd_dq_bf16_kernel<D>>(256, lds));
+  const bool paired =
+      D != 64 && use_pairs(n_tiles, B, Hq, resident_slots<fa_bwd_dq_bf16_kernel<D>>(256, lds));
   const dim3 grid((unsigned)sched_items(paired, n_tiles, B, Hq)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
