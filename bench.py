@@ -207,6 +207,8 @@ def _measure_sq(config: str, out: Path) -> int:
             "mfma_busy": c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * simds),
             "valu_mfma_coexec": c["SQ_VALU_MFMA_COEXEC_CYCLES"] / (gui * simds),
             "lds_bank_conflict_per_active": c["SQ_LDS_BANK_CONFLICT"] / max(c["SQ_LDS_IDX_ACTIVE"], 1.0),
+            "lds_active": c["SQ_LDS_IDX_ACTIVE"] / (gui * simds / 4),
+            "wait_lds_frac": c["SQ_WAIT_INST_LDS"] / max(c["SQ_WAVE_CYCLES"], 1.0),
             "valu_insts_per_wave": c["SQ_INSTS_VALU"] / waves,
             "mfma_insts_per_wave": c["SQ_INSTS_MFMA"] / waves,
             "lds_insts_per_wave": c["SQ_INSTS_LDS"] / waves,
@@ -218,7 +220,8 @@ def _measure_sq(config: str, out: Path) -> int:
         rows.append(f"{sym:<32}{r['mfma_busy']:>9.3f}{r['valu_mfma_coexec']:>9.3f}"
                     f"{r['lds_bank_conflict_per_active']:>9.3f}{r['valu_insts_per_wave']:>9.0f}"
                     f"{r['mfma_insts_per_wave']:>7.0f}{r['lds_insts_per_wave']:>7.0f}"
-                    f"{r['salu_insts_per_wave']:>7.0f}{r['wait_inst_any_frac']:>8.3f}")
+                    f"{r['salu_insts_per_wave']:>7.0f}{r['wait_inst_any_frac']:>8.3f}"
+                    f"{r['lds_active']:>8.3f}{r['wait_lds_frac']:>8.3f}")
     lines = [
         f"# SQ activity per attention kernel, workload {config} (rocprofv3 --pmc, two passes)",
         "# command: python bench.py --measure-sq --config " + config,
@@ -228,7 +231,10 @@ def _measure_sq(config: str, out: Path) -> int:
         "# coex = SQ_VALU_MFMA_COEXEC_CYCLES on the same base: cycles a VALU op issued under a busy MFMA",
         "# bank = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE: LDS cycles lost to bank conflicts per active cycle",
         "# per-wave instruction counts; wait = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES",
-        f"{'kernel':<32}{'mfma':>9}{'coex':>9}{'bank':>9}{'VALU/w':>9}{'MFMA':>7}{'LDS':>7}{'SALU':>7}{'wait':>8}",
+        "# lds = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE/8 x 256 CUs): share of cycles the CU's LDS works on",
+        "#   indexed accesses; wlds = SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES",
+        f"{'kernel':<32}{'mfma':>9}{'coex':>9}{'bank':>9}{'VALU/w':>9}{'MFMA':>7}{'LDS':>7}{'SALU':>7}{'wait':>8}"
+        f"{'lds':>8}{'wlds':>8}",
         *rows,
         "JSON " + json.dumps({"config": config, "kernels": summary}),
     ]

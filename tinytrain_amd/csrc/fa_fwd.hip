@@ -165,8 +165,6 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
   const auto rq = make_rsrc(hd.q, head_bytes);
-  const auto rk = make_rsrc(hd.k, head_bytes);
-  const auto rv = make_rsrc(hd.v, head_bytes);
 
   // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
   // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
