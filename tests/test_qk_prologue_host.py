@@ -190,10 +190,11 @@ def test_abi_rejects_bad_eps(eps):
 @needs_lib
 def test_workspace_bytes():
     lib = _lib.load()
-    # D=128: 16 rows in flight x 4 rounds = 64 rows per workgroup
+    # backward at D=128: 16 rows in flight x 8 rounds = 128 rows per workgroup, one fp32
+    # partial of D values per q or k workgroup
     B, T, Hq, Hkv, D = 2, 100, 8, 2, 128
-    nq = -(-B * T * Hq // 64)
-    nk = -(-B * T * Hkv // 64)
+    nq = -(-B * T * Hq // 128)
+    nk = -(-B * T * Hkv // 128)
     assert lib.ttfa_qk_prologue_workspace_bytes(B, T, Hq, Hkv, D) == (nq + nk) * D * 4
     assert lib.ttfa_qk_prologue_workspace_bytes(B, T, Hq, Hkv, 96) == -1
 

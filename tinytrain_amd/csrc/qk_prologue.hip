@@ -39,13 +39,16 @@ namespace ttfa {
 
 namespace {
 
-constexpr int kRounds = 4;
+constexpr int kRounds = 4;      // forward: row-group rounds per workgroup
+constexpr int kBwdRounds = 8;   // backward: more rows per workgroup, fewer weight-gradient
+                                // partials for the second kernel to add
 
-template <int D>
+template <int D, int R = kRounds>
 struct PShape {
   static constexpr int L = D / 8;               // lanes per row
   static constexpr int GROUPS = 256 / L;         // rows in flight per workgroup
-  static constexpr int ROWS = GROUPS * kRounds;  // rows per workgroup
+  static constexpr int ROUNDS = R;
+  static constexpr int ROWS = GROUPS * R;        // rows per workgroup
 };
 
 __device__ __forceinline__ float bf16_round(float x) { return (float)(bf16)x; }
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(
     const float *__restrict__ rstd_q, const float *__restrict__ rstd_k, bf16 *__restrict__ dq_raw,
     bf16 *__restrict__ dk_raw, bf16 *__restrict__ dv_raw, float *__restrict__ partial, int B,
     int T, int Hq, int Hkv, int nq_wg, int nk_wg) {
-  using S = PShape<D>;
+  using S = PShape<D, kBwdRounds>;
   constexpr int L = S::L;
   __shared__ float red[S::GROUPS][D + 4];
   const int lane = threadIdx.x % L, group = threadIdx.x / L;
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(
     }
   }
 #pragma unroll 1
-  for (int rd = 0; rd < kRounds; ++rd) {
+  for (int rd = 0; rd < S::ROUNDS; ++rd) {
     const int64_t row = (int64_t)wg * S::ROWS + rd * S::GROUPS + group;
     if (row >= n_rows) break;
     const int h = (int)(row % H);
@@ -243,29 +246,32 @@ __global__ __launch_bounds__(256) void qk_prologue_bwd_kernel(
   }
 }
 
-// dw_q = sum of the q workgroups' partials, dw_k of the k workgroups'.  One 1024-thread
-// block per weight vector: thread (slice, col) adds partials slice, slice + S, ... in
-// index order (independent loads, unrolled, so many are in flight), then the S slice
-// sums of each column are added in slice order through LDS: a fixed summation order,
-// so the result is the same on every call.
+// dw_q = sum of the q workgroups' partials, dw_k of the k workgroups'.  2 * D / 16
+// workgroups of 1024 threads; workgroup (vector, column slice) owns 16 columns of one
+// weight vector: thread (slice, col) adds partials slice, slice + 64, ... in index order
+// (independent loads, unrolled, so many are in flight), then the 64 slice sums of each
+// column are added in slice order through LDS.  Every column's summation order is fixed,
+// so the result is the same on every call; spreading the columns over 16 workgroups
+// reads the partials with 16 CUs instead of 2.
 template <int D>
 __global__ __launch_bounds__(1024) void qk_prologue_dw_kernel(const float *__restrict__ partial,
                                                               float *__restrict__ dwq,
                                                               float *__restrict__ dwk, int nq_wg,
                                                               int nk_wg) {
-  constexpr int S = 1024 / D;
-  __shared__ float red[S][D];
-  const int col = threadIdx.x % D, slice = threadIdx.x / D;
-  const int lo = blockIdx.x == 0 ? 0 : nq_wg, n = blockIdx.x == 0 ? nq_wg : nk_wg;
+  constexpr int C = 16, S = 1024 / C;
+  __shared__ float red[S][C + 1];
+  const int which = blockIdx.x / (D / C), c0 = (blockIdx.x % (D / C)) * C;
+  const int col = threadIdx.x % C, slice = threadIdx.x / C;
+  const int lo = which == 0 ? 0 : nq_wg, n = which == 0 ? nq_wg : nk_wg;
   float acc = 0.f;
 #pragma unroll 8
-  for (int i = slice; i < n; i += S) acc += partial[(int64_t)(lo + i) * D + col];
+  for (int i = slice; i < n; i += S) acc += partial[(int64_t)(lo + i) * D + c0 + col];
   red[slice][col] = acc;
   __syncthreads();
-  if (slice == 0) {
+  if (threadIdx.x < C) {
     float tot = 0.f;
-    for (int j = 0; j < S; ++j) tot += red[j][col];
-    (blockIdx.x == 0 ? dwq : dwk)[col] = tot;
+    for (int j = 0; j < S; ++j) tot += red[j][threadIdx.x];
+    (which == 0 ? dwq : dwk)[c0 + threadIdx.x] = tot;
   }
 }
 
@@ -273,9 +279,9 @@ struct Grid {
   int nq, nk, nv;
 };
 
-template <int D>
+template <int D, int R = kRounds>
 Grid prologue_grid(int B, int T, int Hq, int Hkv) {
-  const int64_t rows = PShape<D>::ROWS;
+  const int64_t rows = PShape<D, R>::ROWS;
   auto n = [&](int H) { return (int)(((int64_t)B * T * H + rows - 1) / rows); };
   return {n(Hq), n(Hkv), n(Hkv)};
 }
@@ -330,7 +336,8 @@ int ttfa_qk_prologue_fwd(const void *q_raw, const void *k_raw, const void *v_raw
 
 long long ttfa_qk_prologue_workspace_bytes(int B, int T, int Hq, int Hkv, int D) {
   if (check_prologue(B, T, Hq, Hkv, D)) return -1;
-  const Grid g = D == 64 ? prologue_grid<64>(B, T, Hq, Hkv) : prologue_grid<128>(B, T, Hq, Hkv);
+  const Grid g = D == 64 ? prologue_grid<64, kBwdRounds>(B, T, Hq, Hkv)
+                         : prologue_grid<128, kBwdRounds>(B, T, Hq, Hkv);
   return (long long)(g.nq + g.nk) * D * (long long)sizeof(float);
 }
 
@@ -354,13 +361,14 @@ int ttfa_qk_prologue_bwd(const void *dq, const void *dk, const void *dv, const v
         g.nk);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    dwk_kern<<<dim3(2), dim3(1024), 0, st>>>(workspace, dq_norm_w, dk_norm_w, g.nq, g.nk);
+    dwk_kern<<<dim3(2 * D / 16), dim3(1024), 0, st>>>(workspace, dq_norm_w, dk_norm_w, g.nq,
+                                                       g.nk);
     return (int)hipGetLastError();
   };
   return D == 64 ? go(qk_prologue_bwd_kernel<64>, qk_prologue_dw_kernel<64>,
-                      prologue_grid<64>(B, T, Hq, Hkv))
+                      prologue_grid<64, kBwdRounds>(B, T, Hq, Hkv))
                  : go(qk_prologue_bwd_kernel<128>, qk_prologue_dw_kernel<128>,
-                      prologue_grid<128>(B, T, Hq, Hkv));
+                      prologue_grid<128, kBwdRounds>(B, T, Hq, Hkv));
 }
 
 }  // extern "C"
