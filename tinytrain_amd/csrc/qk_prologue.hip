@@ -14,8 +14,9 @@
 // Work split: a row is one (b, t, head) vector of D bf16, handled by D/8 lanes holding
 // 8 consecutive elements (16 bytes) each; the RoPE partner of element i (i +- D/2) sits
 // in lane ^ D/16 of the same row group.  A 256-thread workgroup runs 256/(D/8) rows at a
-// time for kRounds rounds; workgroups are ordered q rows, then k rows, then v rows, each
-// in the inputs' [B, T, H] row order (contiguous 16-byte loads).
+// time for kRounds (forward) or kBwdRounds (backward) rounds; workgroups are ordered q
+// rows, then k rows, then v rows, each in the inputs' [B, T, H] row order (contiguous
+// 16-byte loads).
 //
 // Backward (autograd of the same expressions; the bf16 roundings pass gradients
 // through unchanged): RoPE^T, dy_i = g_i c_i + (i < D/2 ? g_{i+D/2} s_{i+D/2}
