@@ -56,7 +56,7 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
     """
     import torch
 
-    from oracle.eager_attention import eager_attention_grads
+    from oracle.eager_attention import eager_attention, eager_attention_grads
     from tinytrain_amd.workloads import make_inputs
 
     threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -83,22 +83,37 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
     t1 = run(1)
     b = max(1, min(cfg.B, int(1.0 / max(t1, 1e-6))))
     times, spent = [], 0.0
-    while spent < budget_s or len(times) < 3:
+    while spent < 0.75 * budget_s or len(times) < 3:
         t = run(b)
         times.append(t)
         spent += t
         if len(times) >= 400:
             break
     med = statistics.median(times)
+    # forward alone (no autograd graph), same slice, the rest of the budget
+    ftimes, fspent = [], 0.0
+    with torch.no_grad():
+        while fspent < 0.25 * budget_s or len(ftimes) < 3:
+            t0 = time.perf_counter()
+            eager_attention(q[:b], k[:b], v[:b])
+            ftimes.append(time.perf_counter() - t0)
+            fspent += ftimes[-1]
+            if len(ftimes) >= 400:
+                break
+    fmed = statistics.median(ftimes)
     flop = 3.5 * cfg.fwd_flop() * b / cfg.B
     return {
         "value": round(flop / med / 1e12, 5),
+        "forward_tflops": round(cfg.fwd_flop() * b / cfg.B / fmed / 1e12, 5),
+        "seconds_full_workload": {"fwd": round(fmed * cfg.B / b, 4),
+                                  "fwd_bwd": round(med * cfg.B / b, 4)},
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"{cfg.name} batch slice b={b} of B={cfg.B} (same seeded inputs), fp32 "
                    f"repeat_interleave + causal SDPA forward + autograd backward on the CPU, "
-                   f"median of {len(times)} runs ({spent:.1f} s of CPU work)"),
+                   f"median of {len(times)} runs ({spent:.1f} s of CPU work); forward alone "
+                   f"(no grad) median of {len(ftimes)} runs ({fspent:.1f} s)"),
         "seconds_per_sample": round(med, 4),
         "cpu_model": _cpu_model(),
         "logical_cpus_visible": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count(),
