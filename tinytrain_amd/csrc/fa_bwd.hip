@@ -4,20 +4,25 @@
 // :208-209) instead of storing it:
 //
 //  1. dQ pass (reference: bwd_preprocess :70-90 fused with bwd_dq_kernel :162-217).
-//     A row tile = 128 query rows of one (batch, head), 4 waves x 32 rows; each
-//     workgroup takes a balanced pair of row tiles, the longer first (pair_item).
+//     A row tile = 128 query rows of one (batch, head), 4 waves x 32 rows.  At D = 128
+//     a workgroup takes a balanced pair of row tiles, the longer first (pair_item), when
+//     pairs fill whole rounds of the resident slots; at D = 64 it takes one row tile,
+//     longest first, so the row body is inlined once and three workgroups per CU fit
+//     without spills.
 //     The prologue computes Delta = rowsum(O * dO) for the tile's own rows from the
 //     same registers that hold dO, and writes it to the workspace
 //     for pass 2 (so there is no separate preprocess launch and dO is read once here).
-//     Per key tile from LDS (64 keys for D=64, 32 for D=128):  S^T = K Q^T and
+//     Per key tile from LDS (64 keys for D=64, 32 for D=128), one 32-key block at a time:
+//     S^T = K Q^T and
 //     dP^T - Delta = V dO^T - Delta (the dP accumulator starts at -Delta, a per-lane
 //     constant, so dS costs one multiply), P^T = exp2(S^T*scale*log2e - LSE*log2e),
 //     dS^T = P^T (dP^T - Delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
 //     Every lane owns one query row, so LSE and Delta are per-lane scalars.
 //
 //  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  A key tile = 128 keys of one
-//     (batch, kv head), 4 waves x 32 keys, and each workgroup takes a balanced pair of
-//     key tiles; the wave's K and V rows stay in registers.
+//     (batch, kv head), 4 waves x 32 keys; a workgroup takes a balanced pair of key
+//     tiles when pairs fill whole rounds of the resident slots, else one key tile,
+//     longest first.  The wave's K and V rows stay in registers.
 //     The workgroup walks the G query heads of its group and, for each, the 64-row Q
 //     tiles from the diagonal to the end, double-buffered through LDS together with the
 //     tiles' -LSE/scale and -Delta; dK and dV accumulate in registers across the whole
@@ -29,8 +34,9 @@
 //     from LDS.  dK is scaled once at the end (:154).
 //
 // Both passes fill their LDS tiles with buffer_load ... lds (global -> LDS, 16 bytes per
-// lane, no staging VGPRs).  Tiles entirely above the diagonal are skipped; only tiles
-// crossing the diagonal or the ragged end of T run the masked body.
+// lane, no staging VGPRs), the next tile's loads in flight while the current tile is
+// computed.  Tiles entirely above the diagonal are skipped; only tiles crossing the
+// diagonal or the ragged end of T run the masked body.
 #include "fa_common.h"
 #include "fa_kernels.h"
 

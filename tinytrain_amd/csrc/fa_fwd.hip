@@ -6,7 +6,8 @@
 //
 // Work split: one workgroup = 4 waves; a row tile is 128 query rows of one (batch, head)
 // and each wave owns 32 of them.  A workgroup processes a pair of row tiles, the longer
-// first, so every workgroup carries the same causal work (pair_item).  K/V stream
+// first, so every workgroup carries the same causal work (pair_item), when pairs fill
+// whole rounds of the resident slots; otherwise single tiles, longest first.  K/V stream
 // through LDS in 64-key tiles, double-buffered: the next tile's global loads are in
 // flight while the current tile is consumed.  The loads go from the buffer straight
 // into LDS (buffer_load ... lds, 16 bytes per lane), so no VGPRs stage them.
