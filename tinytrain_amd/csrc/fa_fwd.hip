@@ -170,8 +170,8 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
   // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
   // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
   // holds logical chunk phys ^ swizzle(row).  The lane's offset within a tile is fixed
-  // (voffset); the tile's start is the scalar soffset; the LDS destination (M0) comes
-  // from the scalar wave index.
+  // (voffset); the tile's start goes into a descriptor re-based per tile (scalar work);
+  // the LDS destination (M0) comes from the scalar wave index.
   const int wave_s = wave_id();
   uint32_t voff[LOADS];
 #pragma unroll
