@@ -69,6 +69,34 @@ def test_decode_agrees_with_forward_kernel():
     assert_close_abs("LSE", lse, lse_full[:, :, T - Tq:], TOL_LSE)
 
 
+@pytest.mark.parametrize("B, L", [(32, 4096), (1, 16384), (128, 1024)])
+def test_decode_bench_shapes_match_forward(B, L):
+    """At the decode bench's shapes (Hq 16, Hkv 8, D 128; hundreds of key splits per row
+    at B=1), the decoded row of every batch equals row cache_len-1 of the batched forward
+    kernel over the whole cache, for per-batch cache lengths."""
+    announce(f"decode bench shape B={B} L={L}")
+    Hq, Hkv, D = 16, 8, 128
+    g = torch.Generator(device=DEV).manual_seed(3)
+
+    def unit_rms(t):
+        return (t / t.pow(2).mean(-1, keepdim=True).sqrt()).to(torch.bfloat16)
+
+    q = unit_rms(torch.randn(B, Hq, L, D, device=DEV, generator=g))
+    k = unit_rms(torch.randn(B, Hkv, L, D, device=DEV, generator=g))
+    v = torch.randn(B, Hkv, L, D, device=DEV, generator=g).to(torch.bfloat16)
+    lens = torch.randint(1, L + 1, (B,), device=DEV, generator=g, dtype=torch.int32)
+    lens[0] = L
+    o_full, lse_full = _forward(q, k, v)
+    rows = (lens.long() - 1).view(B, 1, 1, 1).expand(B, Hq, 1, D)
+    qd = torch.gather(q, 2, rows).contiguous()
+    o, lse = flash_attn_decode(qd, k, v, lens)
+    want_o = torch.gather(o_full, 2, rows)
+    want_lse = torch.gather(lse_full, 2, (lens.long() - 1).view(B, 1, 1).expand(B, Hq, 1))
+    torch.cuda.synchronize()
+    assert_close_abs("O", o, want_o, TOL[torch.bfloat16])
+    assert_close_abs("LSE", lse, want_lse, TOL_LSE)
+
+
 def test_decode_deterministic_and_opcheck():
     announce("decode determinism + opcheck")
     q, k, v = (t.to(DEV) for t in _inputs(4, 8, 2, 2, 1024, 64, seed=2))

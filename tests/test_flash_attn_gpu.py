@@ -134,6 +134,40 @@ def test_edge_shapes(B, H, H_kv, T, D, dtype):
             torch.testing.assert_close(got.double(), want[i], rtol=3e-2, atol=3e-2)
 
 
+def _random_shapes(n=12, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    while len(out) < n:
+        D = (64, 128)[int(torch.randint(0, 2, (1,), generator=g))]
+        Hkv = int(torch.randint(1, 4, (1,), generator=g))
+        G = int(torch.randint(1, 5, (1,), generator=g))
+        B = int(torch.randint(1, 4, (1,), generator=g))
+        T = int(torch.randint(1, 420, (1,), generator=g))
+        if B * Hkv * G <= 16:
+            out.append((B, Hkv * G, Hkv, T, D))
+    return out
+
+
+@pytest.mark.parametrize("B, H, H_kv, T, D", _random_shapes())
+def test_random_shapes(B, H, H_kv, T, D):
+    """Seeded random shapes (ragged T, group sizes 1-4, both head dims) on the
+    configurations' input distribution: unit-RMS q and k, v ~ N(0,1), dO ~ N(0,1) * 1e-2;
+    every output within the attention tolerances of the fp64 oracle."""
+    announce(f"random B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    g = torch.Generator().manual_seed(B * 1000 + H * 100 + T + D)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = torch.randn(B, H_kv, T, D, generator=g)
+    q = q / q.pow(2).mean(-1, keepdim=True).sqrt()
+    k = k / k.pow(2).mean(-1, keepdim=True).sqrt()
+    v = torch.randn(B, H_kv, T, D, generator=g)
+    do = torch.randn(B, H, T, D, generator=g) * 1e-2
+    q, k, v, do = (t.to(torch.bfloat16) for t in (q, k, v, do))
+    got = _run(q, k, v, do)
+    want = reference_outputs(q, k, v, do, dtype=torch.float64)
+    for nm, a, b in zip(("o", "lse", "dq", "dk", "dv"), got, want):
+        assert_close_abs(nm, a, b, TOL_LSE if nm == "lse" else TOL[torch.bfloat16])
+
+
 def _poisoned_call(q, k, v, do):
     """Call the C ABI with NaN-filled outputs: every element must be overwritten."""
     lib = _lib.load()
