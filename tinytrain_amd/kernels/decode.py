@@ -62,9 +62,10 @@ def flash_attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Ten
     ws = torch.empty((nbytes // 4 + 4,), device=q.device, dtype=torch.float32)
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, Tq), device=q.device, dtype=torch.float32)
+    seqlens = cache_seqlens.contiguous()  # held until the launch is enqueued
     with torch.cuda.device(q.device):
         _lib.check(lib.ttfa_decode_fwd(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                       cache_seqlens.contiguous().data_ptr(), o.data_ptr(),
+                                       seqlens.data_ptr(), o.data_ptr(),
                                        lse.data_ptr(), ws.data_ptr(), B, Hq, Hkv, Tq, L, D,
                                        _lib.TTFA_BF16, 1.0 / math.sqrt(D),
                                        torch.cuda.current_stream(q.device).cuda_stream))
