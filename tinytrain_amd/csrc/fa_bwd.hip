@@ -219,7 +219,7 @@ struct DqHead {
 // workgroup barrier, so the caller may reuse the LDS ring right away.
 template <int D>
 __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, float scale_log2,
-                                        float scale, int work_left, int work_max) {
+                                        float scale) {
   using P = DqTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   const int T = hd.T;
@@ -297,9 +297,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqacc[db] = f32x16{};
 
-  PrioByRemaining prio(work_max);
+  // No issue-priority steering here (the forward uses it): measured, it slowed both
+  // backward passes.
   for (int j = 0; j < n_kv; ++j) {
-    prio.update(work_left - j);
     if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
     const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
     if (j < n_full)
@@ -327,22 +327,16 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_bf16_kernel(
   using P = DqTile<D>;
   const int n_tiles = (T + P::BM - 1) / P::BM;
   const WorkPair w = sched_item(paired, blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
-  // Key tiles a row tile visits is its work; the priority scales by the largest
-  // workgroup's work.
-  const int n_kt = (T + P::BN - 1) / P::BN;
-  auto work = [&](int qt) { return qt < 0 ? 0 : min(n_kt, (qt + 1) * (P::BM / P::BN)); };
-  const int w1 = work(w.first), w2 = work(w.second);
-  const int wmax = paired ? work(n_tiles - 1) + work(0) : work(n_tiles - 1);
   const int G = Hq / Hkv;
   const int b = w.bh / Hq, h = w.bh - b * Hq;
   const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D, qb = w.bh * hs;
   const DqHead hd{Q + qb, K + kvh * hs, V + kvh * hs, O + qb, dO + qb,
                   LSE + (int64_t)w.bh * T, Delta + (int64_t)w.bh * T, dQ + qb, T};
-  dq_rows<D>(smem, hd, w.first, scale_log2, scale, w1 + w2, wmax);
+  dq_rows<D>(smem, hd, w.first, scale_log2, scale);
   // D = 64 runs single tiles only (the launcher never pairs it): a second inlined copy of
   // the row body would not fit three workgroups per CU without spills, and the spill
   // reloads wait on the tile prefetch.  Longest-first singles balance as well here.
-  if (D != 64 && w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
+  if (D != 64 && w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale);
 }
 
 // Packed variable-length sequences ([H, total, D], sequence s at rows cu_seqlens[s] ..
@@ -354,7 +348,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, const int *__restrict__ cu_seqlens,
-    int n_seq, int total, int Hq, int Hkv, int max_tiles, float scale_log2, float scale) {
+    int n_seq, int total, int Hq, int Hkv, float scale_log2, float scale) {
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
   using P = DqTile<D>;
   const int per_rank = n_seq * Hq;
@@ -366,13 +360,11 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
   const int n_tiles = (T + P::BM - 1) / P::BM;
   if (rank >= n_tiles) return;
   const int qt = n_tiles - 1 - rank;
-  const int n_kt = (T + P::BN - 1) / P::BN;
-  const int wmax = max_tiles * (P::BM / P::BN);
   const int hk = h / (Hq / Hkv);
   const int64_t qb = ((int64_t)h * total + c0) * D, kb = ((int64_t)hk * total + c0) * D;
   const int64_t rb = (int64_t)h * total + c0;
   const DqHead hd{Q + qb, K + kb, V + kb, O + qb, dO + qb, LSE + rb, Delta + rb, dQ + qb, T};
-  dq_rows<D>(smem, hd, qt, scale_log2, scale, min(n_kt, (qt + 1) * (P::BM / P::BN)), wmax);
+  dq_rows<D>(smem, hd, qt, scale_log2, scale);
 }
 
 // ---------------------------------------------------------------- pass 2: dK, dV
@@ -393,7 +385,7 @@ struct DkvHead {
 // right away.
 template <int D>
 __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, float scale_log2,
-                                          float scale, int work_left, int work_max) {
+                                          float scale) {
   using P = DkvTile<D>;
   constexpr int BNK = P::BNK, BMQ = P::BMQ, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   float *const ldsf = reinterpret_cast<float *>(lds + 2 * 2 * BMQ * D);
@@ -472,10 +464,8 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
   __syncthreads();
-  PrioByRemaining prio(work_max);
   int qt = qt_lo;  // query tile of the current item
   for (int it = 0; it < n_items; ++it) {
-    prio.update(work_left - it);
     if (it + 1 < n_items) load_item((it + 1) & 1);
     const int stage = it & 1;
     const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
@@ -522,19 +512,13 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kerne
   const int n_ktiles = (T + P::BNK - 1) / P::BNK;
   // Key tile 0 sees the most query rows, so the longer tile of a pair is the low one.
   const WorkPair w = sched_item(paired, blockIdx.x, n_ktiles, B, Hkv, 1, true);
-  // Query tiles a key tile visits (times the group's query heads) is its work; the
-  // priority scales by the largest workgroup's work.
-  const int n_qt = (T + P::BMQ - 1) / P::BMQ;
   const int G = Hq / Hkv;
-  auto work = [&](int kt) { return kt < 0 ? 0 : G * (n_qt - kt * (P::BNK / P::BMQ)); };
-  const int w1 = work(w.first), w2 = work(w.second);
-  const int wmax = paired ? work(0) + work(n_ktiles - 1) : work(0);
   const int b = w.bh / Hkv, hk = w.bh - b * Hkv;
   const int64_t hs = (int64_t)T * D, kvb = w.bh * hs, q0 = (int64_t)b * Hq + hk * G;
   const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs, dO + q0 * hs,
                    LSE + q0 * T, Delta + q0 * T, hs, T, G, T};
-  dkdv_rows<D>(smem, hd, w.first, scale_log2, scale, w1 + w2, wmax);
-  if (w.second >= 0) dkdv_rows<D>(smem, hd, w.second, scale_log2, scale, w2, wmax);
+  dkdv_rows<D>(smem, hd, w.first, scale_log2, scale);
+  if (w.second >= 0) dkdv_rows<D>(smem, hd, w.second, scale_log2, scale);
 }
 
 // Packed variable-length sequences (layouts as for the varlen dQ pass).  Workgroup ->
@@ -545,8 +529,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV,
-    const int *__restrict__ cu_seqlens, int n_seq, int total, int Hq, int Hkv, int max_ktiles,
-    float scale_log2, float scale) {
+    const int *__restrict__ cu_seqlens, int n_seq, int total, int Hq, int Hkv, float scale_log2,
+    float scale) {
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
   using P = DkvTile<D>;
   const int per_rank = n_seq * Hkv;
@@ -557,14 +541,12 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
   const int T = c1 - c0;
   if (kt >= (T + P::BNK - 1) / P::BNK) return;
   const int G = Hq / Hkv;
-  const int n_qt = (T + P::BMQ - 1) / P::BMQ;
-  const int wmax = G * max_ktiles * (P::BNK / P::BMQ);
   const int64_t hs = (int64_t)total * D, kvb = (int64_t)hk * hs + (int64_t)c0 * D;
   const int64_t q0 = (int64_t)hk * G;
   const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs + (int64_t)c0 * D,
                    dO + q0 * hs + (int64_t)c0 * D, LSE + q0 * total + c0,
                    Delta + q0 * total + c0, hs, total, G, T};
-  dkdv_rows<D>(smem, hd, kt, scale_log2, scale, G * (n_qt - kt * (P::BNK / P::BMQ)), wmax);
+  dkdv_rows<D>(smem, hd, kt, scale_log2, scale);
 }
 
 template <typename Kern>
@@ -629,8 +611,7 @@ static hipError_t launch_dq_varlen(const void *q, const void *k, const void *v, 
   const dim3 grid((unsigned)((int64_t)max_tiles * n_seq * Hq)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
-                                     cu_seqlens, n_seq, total, Hq, Hkv, max_tiles, scale * kLog2e,
-                                     scale);
+                                     cu_seqlens, n_seq, total, Hq, Hkv, scale * kLog2e, scale);
   return hipGetLastError();
 }
 
@@ -650,8 +631,7 @@ static hipError_t launch_dkdv_varlen(const void *q, const void *k, const void *v
   const dim3 grid((unsigned)((int64_t)max_ktiles * n_seq * Hkv)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv,
-                                     cu_seqlens, n_seq, total, Hq, Hkv, max_ktiles,
-                                     scale * kLog2e, scale);
+                                     cu_seqlens, n_seq, total, Hq, Hkv, scale * kLog2e, scale);
   return hipGetLastError();
 }
 
