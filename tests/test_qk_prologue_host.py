@@ -7,7 +7,6 @@ validation paths and the Python op surface are checked without a GPU (validation
 returns before any HIP call).
 """
 
-import ctypes
 import math
 
 import pytest

@@ -10,7 +10,6 @@ and the CPU oracle.
   rows of sequences with invalid bounds are left unwritten; opcheck and autograd.
 """
 
-import math
 
 import pytest
 import torch
