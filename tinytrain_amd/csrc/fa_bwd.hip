@@ -549,11 +549,20 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
   dkdv_rows<D>(smem, hd, kt, scale_log2, scale);
 }
 
-template <typename Kern>
-static hipError_t allow_lds(Kern kern, size_t bytes) {
-  // Idempotent; needed once per kernel for more than 64 KiB of dynamic LDS.
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+// Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,
+// including launches under stream capture, make no attribute call.
+template <auto KERN>
+static hipError_t allow_lds(size_t bytes) {
+  static std::atomic<uint64_t> done{0};  // bit d: set on device d
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t{1} << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return e;
 }
 
 template <int D>
@@ -564,7 +573,7 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
   constexpr size_t lds = DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_bf16_kernel<D>;
   if (lds > 65536) {
-    hipError_t e = allow_lds(kern, lds);
+    hipError_t e = allow_lds<fa_bwd_dq_bf16_kernel<D>>(lds);
     if (e != hipSuccess) return e;
   }
   const bool paired =
@@ -584,7 +593,7 @@ static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const
   constexpr size_t lds = DkvTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dkdv_bf16_kernel<D>;
   if (lds > 65536) {
-    hipError_t e = allow_lds(kern, lds);
+    hipError_t e = allow_lds<fa_bwd_dkdv_bf16_kernel<D>>(lds);
     if (e != hipSuccess) return e;
   }
   const bool paired =
@@ -605,7 +614,7 @@ static hipError_t launch_dq_varlen(const void *q, const void *k, const void *v, 
   constexpr size_t lds = DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_varlen_bf16_kernel<D>;
   if (lds > 65536) {
-    hipError_t e = allow_lds(kern, lds);
+    hipError_t e = allow_lds<fa_bwd_dq_varlen_bf16_kernel<D>>(lds);
     if (e != hipSuccess) return e;
   }
   const dim3 grid((unsigned)((int64_t)max_tiles * n_seq * Hq)), block(256);
@@ -625,7 +634,7 @@ static hipError_t launch_dkdv_varlen(const void *q, const void *k, const void *v
   constexpr size_t lds = DkvTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dkdv_varlen_bf16_kernel<D>;
   if (lds > 65536) {
-    hipError_t e = allow_lds(kern, lds);
+    hipError_t e = allow_lds<fa_bwd_dkdv_varlen_bf16_kernel<D>>(lds);
     if (e != hipSuccess) return e;
   }
   const dim3 grid((unsigned)((int64_t)max_ktiles * n_seq * Hkv)), block(256);
