@@ -60,12 +60,12 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (TTFA_LDS void *)lds_wave, 16, byte_off, 0, 0, 0);
 }
 
-// Index of the calling wave in its workgroup as a wave-uniform (scalar) value, so LDS
-// addresses derived from it stay in SGPRs (M0 of the LDS-direct loads needs no
-// v_readfirstlane per load).
 // s_waitcnt vmcnt(0): every vector memory load of this wave (direct-to-LDS included) done.
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Index of the calling wave in its workgroup as a wave-uniform (scalar) value, so LDS
+// addresses derived from it stay in SGPRs (M0 of the LDS-direct loads needs no
+// v_readfirstlane per load).
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // LDS tiles are row-major [rows][D] bf16, stored in 16-byte chunks whose index is
