@@ -167,6 +167,29 @@ def test_random_shapes(B, H, H_kv, T, D):
         assert_close_abs(nm, a, b, TOL_LSE if nm == "lse" else TOL[torch.bfloat16])
 
 
+@pytest.mark.parametrize("B, H, H_kv, T, D", [
+    (1, 16, 1, 300, 64),    # MQA: one KV head for 16 query heads
+    (2, 16, 2, 200, 128),   # G=8
+    (1, 32, 4, 130, 64),    # G=8, T one row past a 128-row tile
+])
+def test_large_groups(B, H, H_kv, T, D):
+    """Query-head groups of 8 and 16: the dK/dV pass reduces over the whole group in its
+    item loop, and every query head reads KV head h // G."""
+    announce(f"large group B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    g = torch.Generator().manual_seed(H * 100 + T + D)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = torch.randn(B, H_kv, T, D, generator=g)
+    q = q / q.pow(2).mean(-1, keepdim=True).sqrt()
+    k = k / k.pow(2).mean(-1, keepdim=True).sqrt()
+    v = torch.randn(B, H_kv, T, D, generator=g)
+    do = torch.randn(B, H, T, D, generator=g) * 1e-2
+    q, k, v, do = (t.to(torch.bfloat16) for t in (q, k, v, do))
+    got = _run(q, k, v, do)
+    want = reference_outputs(q, k, v, do, dtype=torch.float64)
+    for nm, a, b in zip(("o", "lse", "dq", "dk", "dv"), got, want):
+        assert_close_abs(nm, a, b, TOL_LSE if nm == "lse" else TOL[torch.bfloat16])
+
+
 def _poisoned_call(q, k, v, do):
     """Call the C ABI with NaN-filled outputs: every element must be overwritten."""
     lib = _lib.load()
