@@ -32,6 +32,8 @@ constexpr float kDecodeSlack = 8.0f;
 constexpr int kDecBlock = 32;  // keys per block
 constexpr int kDecWaves = 4;   // ranges (waves) per workgroup
 constexpr int kDecMaxSplits = 512;  // partials per query row, at most
+constexpr int kCombinePrefetch = 16;  // partial rows per merge thread loaded up front ...
+constexpr int kCombinePrefetchMin = 64;  // ... when a row has at least this many partials
 
 template <int D>
 struct DecShape {
@@ -213,12 +215,14 @@ __global__ __launch_bounds__(256, 2) void fa_decode_bf16_kernel(
 
 // Merge the n_splits partials of every query row: M = max m over partials with l > 0,
 // O = sum o_s 2^(m_s - M) / sum l_s 2^(m_s - M), LSE = (M + log2 sum) ln 2; a row with no
-// visible key gets O = 0, LSE = -inf.  One 256-thread workgroup per row: the threads
-// split the partials for M and the weights (kept in LDS); then thread t sums float4
-// column t % (D/4) over the partials s = t / (D/4) (mod 256 / (D/4)), loads issued
-// unconditionally (a partial without keys holds zeros and weight 0), and the groups are
-// added in a fixed order, so the result does not depend on timing.
-template <int D>
+// visible key gets O = 0, LSE = -inf.  One 256-thread workgroup per row: thread t sums
+// float4 column t % (D/4) over the partials s = t / (D/4) (mod 256 / (D/4)).  With PF > 0
+// (rows with many partials) its first PF partial rows and its (m, l) pair are loaded
+// before anything waits, so the row takes one memory round trip; then the threads reduce
+// M and the weights (kept in LDS), and the partials are weighted (a partial without keys
+// holds zeros and weight 0) and the groups added in a fixed order, so the result does not
+// depend on timing (nor on PF).
+template <int D, int PF>
 __global__ __launch_bounds__(256) void fa_decode_combine_kernel(
     const float *__restrict__ part_o, const float *__restrict__ part_ml, bf16 *__restrict__ O,
     float *__restrict__ LSE, int rows, int n_splits) {
@@ -228,8 +232,17 @@ __global__ __launch_bounds__(256) void fa_decode_combine_kernel(
   __shared__ f32x4 accs[SG][C4];
   const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float *ml = part_ml + (int64_t)row * n_splits * 2;
-  float M = -INFINITY;
-  for (int s = tid; s < n_splits; s += 256) {
+  const int c = tid % C4, sg = tid / C4;
+  const f32x4 *po = reinterpret_cast<const f32x4 *>(part_o + (int64_t)row * n_splits * D) + c;
+  f32x4 xs[PF > 0 ? PF : 1];
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const int s = sg + j * SG;
+    xs[j] = s < n_splits ? po[(int64_t)s * C4] : f32x4{};
+  }
+  const f32x2 v0 = tid < n_splits ? *reinterpret_cast<const f32x2 *>(ml + 2 * tid) : f32x2{0.f, 0.f};
+  float M = v0[1] > 0.f ? v0[0] : -INFINITY;
+  for (int s = tid + 256; s < n_splits; s += 256) {
     const f32x2 v = *reinterpret_cast<const f32x2 *>(ml + 2 * s);
     if (v[1] > 0.f) M = fmax2(M, v[0]);
   }
@@ -240,7 +253,7 @@ __global__ __launch_bounds__(256) void fa_decode_combine_kernel(
   M = fmax2(fmax2(red[0], red[1]), fmax2(red[2], red[3]));
   float lsum = 0.f;
   for (int s = tid; s < n_splits; s += 256) {
-    const f32x2 v = *reinterpret_cast<const f32x2 *>(ml + 2 * s);
+    const f32x2 v = s == tid ? v0 : *reinterpret_cast<const f32x2 *>(ml + 2 * s);
     const float w = (v[1] > 0.f && M != -INFINITY) ? exp2f_fast(v[0] - M) : 0.f;
     wts[s] = w;
     lsum = __builtin_fmaf(v[1] > 0.f ? v[1] : 0.f, w, lsum);
@@ -250,11 +263,16 @@ __global__ __launch_bounds__(256) void fa_decode_combine_kernel(
   if (lane == 0) red[4 + wave] = lsum;
   __syncthreads();  // wts and the sums are visible
   lsum = (red[4] + red[5]) + (red[6] + red[7]);
-  const int c = tid % C4, sg = tid / C4;
-  const f32x4 *po = reinterpret_cast<const f32x4 *>(part_o + (int64_t)row * n_splits * D) + c;
   f32x4 acc{};
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const int s = sg + j * SG;
+    const float w = s < n_splits ? wts[s] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = w != 0.f ? __builtin_fmaf(xs[j][e], w, acc[e]) : acc[e];
+  }
 #pragma unroll 4
-  for (int s = sg; s < n_splits; s += SG) {
+  for (int s = sg + PF * SG; s < n_splits; s += SG) {
     const f32x4 x = po[(int64_t)s * C4];
     const float w = wts[s];
 #pragma unroll
@@ -306,22 +324,30 @@ hipError_t launch_decode_bf16(const void *q, const void *k_cache, const void *v_
   const float sl2 = scale * kLog2e;
   const dim3 grid((unsigned)((int64_t)B * Hkv * sp.n_chunks)), block(256);
   const dim3 cgrid((unsigned)rows), cblock(256);
+  const bool prefetch = sp.n_splits >= kCombinePrefetchMin;
+  auto combine = [&](auto kern) {
+    kern<<<cgrid, cblock, 0, stream>>>(part_o, part_ml, (bf16 *)o, lse, rows, sp.n_splits);
+  };
   if (D == 64) {
     fa_decode_bf16_kernel<64><<<grid, block, 0, stream>>>(
         (const bf16 *)q, (const bf16 *)k_cache, (const bf16 *)v_cache, cache_seqlens, part_o,
         part_ml, B, Hq, Hkv, Tq, Lmax, sp.n_chunks, sp.wkeys, sl2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    fa_decode_combine_kernel<64><<<cgrid, cblock, 0, stream>>>(part_o, part_ml, (bf16 *)o, lse,
-                                                                rows, sp.n_splits);
+    if (prefetch)
+      combine(fa_decode_combine_kernel<64, kCombinePrefetch>);
+    else
+      combine(fa_decode_combine_kernel<64, 0>);
   } else {
     fa_decode_bf16_kernel<128><<<grid, block, 0, stream>>>(
         (const bf16 *)q, (const bf16 *)k_cache, (const bf16 *)v_cache, cache_seqlens, part_o,
         part_ml, B, Hq, Hkv, Tq, Lmax, sp.n_chunks, sp.wkeys, sl2);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    fa_decode_combine_kernel<128><<<cgrid, cblock, 0, stream>>>(part_o, part_ml, (bf16 *)o, lse,
-                                                                 rows, sp.n_splits);
+    if (prefetch)
+      combine(fa_decode_combine_kernel<128, kCombinePrefetch>);
+    else
+      combine(fa_decode_combine_kernel<128, 0>);
   }
   return hipGetLastError();
 }
