@@ -167,6 +167,24 @@ def test_random_shapes(B, H, H_kv, T, D):
         assert_close_abs(nm, a, b, TOL_LSE if nm == "lse" else TOL[torch.bfloat16])
 
 
+@pytest.mark.parametrize("B, H, H_kv, T, D", _random_shapes(n=6, seed=23))
+def test_random_shapes_fp32(B, H, H_kv, T, D):
+    """The fp32 path (C1's dtype) on seeded random shapes: every output within 1e-5 of
+    the fp64 oracle (LSE within its 1e-3)."""
+    announce(f"random fp32 B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    g = torch.Generator().manual_seed(B * 1000 + H * 100 + T + D + 7)
+    q = torch.randn(B, H, T, D, generator=g)
+    k = torch.randn(B, H_kv, T, D, generator=g)
+    q = q / q.pow(2).mean(-1, keepdim=True).sqrt()
+    k = k / k.pow(2).mean(-1, keepdim=True).sqrt()
+    v = torch.randn(B, H_kv, T, D, generator=g)
+    do = torch.randn(B, H, T, D, generator=g) * 1e-2
+    got = _run(q, k, v, do)
+    want = reference_outputs(q, k, v, do, dtype=torch.float64)
+    for nm, a, b in zip(("o", "lse", "dq", "dk", "dv"), got, want):
+        assert_close_abs(nm, a, b, TOL_LSE if nm == "lse" else TOL[torch.float32])
+
+
 @pytest.mark.parametrize("B, H, H_kv, T, D", [
     (1, 16, 1, 300, 64),    # MQA: one KV head for 16 query heads
     (2, 16, 2, 200, 128),   # G=8
