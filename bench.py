@@ -25,6 +25,7 @@ import math
 import os
 import platform
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -38,13 +39,42 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 
 
 def _cpu_model() -> str:
+    """Host CPU model: lscpu's "Model name" (with family/model/stepping when the name is
+    generic, as on virtualised hosts), else /proc/cpuinfo."""
+    fields = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                key, val = line.split(":", 1)
+                fields[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return platform.processor() or "unknown"
+    name = fields.get("Model name", "")
+    if not name:
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    name = name or platform.processor() or "unknown"
+    ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if k in fields]
+    sockets = fields.get("Socket(s)")
+    extra = ", ".join(ids + ([f"{sockets} socket(s)"] if sockets else []))
+    return f"{name} ({extra})" if extra else name
+
+
+def _cpu_threads() -> tuple[int, int, str]:
+    """(threads to use, logical CPUs visible, why).  All visible CPUs, unless
+    OMP_NUM_THREADS names fewer: a GPU host that shares its cores between GPUs states each
+    GPU's share there (16 per GPU on the MI355X boxes this runs on)."""
+    visible = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < visible:
+        return int(omp), visible, f"OMP_NUM_THREADS={omp} (this GPU's share of the host)"
+    return visible, visible, "all visible logical CPUs"
 
 
 def _cpu_baseline(cfg, budget_s: float) -> dict:
@@ -59,8 +89,7 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
     from oracle.eager_attention import eager_attention, eager_attention_grads
     from tinytrain_amd.workloads import make_inputs
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
+    threads, visible, why = _cpu_threads()
     torch.set_num_threads(threads)
     q, k, v, do, _ = make_inputs(cfg, seed=0)
 
@@ -116,7 +145,8 @@ def _cpu_baseline(cfg, budget_s: float) -> dict:
                    f"(no grad) median of {len(ftimes)} runs ({fspent:.1f} s)"),
         "seconds_per_sample": round(med, 4),
         "cpu_model": _cpu_model(),
-        "logical_cpus_visible": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count(),
+        "logical_cpus_visible": visible,
+        "threads_rule": why,
         "torch_threads": torch.get_num_threads(),
         "sdpa_cpu_ops": backend,
     }

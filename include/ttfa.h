@@ -114,8 +114,12 @@ int ttfa_bwd_dkdv(const void *q, const void *k, const void *v, const void *dout,
  *   cu_seqlens     : [n_seq + 1] int32 in device memory, 4-byte aligned, non-decreasing,
  *                    cu_seqlens[0] = 0, cu_seqlens[n_seq] = total, every length
  *                    <= max_seqlen.  A sequence with bounds outside 0..total or
- *                    decreasing is skipped (its rows are not written); rows of a
- *                    sequence longer than max_seqlen past max_seqlen are not written.
+ *                    decreasing is skipped (its rows are not written).  A sequence
+ *                    longer than max_seqlen is processed as its first max_seqlen tokens,
+ *                    the same way in the forward and in both backward passes: o, lse,
+ *                    dq, dk and dv of those rows are exact (a causal row depends only on
+ *                    earlier keys) and its rows from position max_seqlen on are not
+ *                    written.
  * Validation as above, plus TTFA_E_DTYPE for anything but TTFA_BF16 and TTFA_E_SEQ
  * for n_seq, total or max_seqlen < 1.  Results for each sequence are bitwise those of
  * ttfa_fwd / ttfa_bwd on that sequence alone (B = 1, T = its length).

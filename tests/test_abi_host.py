@@ -220,6 +220,34 @@ def test_hip_switch_on_cpu_fails_loudly():
         causal_attention(q, q, q, "hip")
 
 
+def test_reference_import_path_reexports_the_same_ops():
+    """`from kernels.flash_attn import ...` (model.py:6, tests/test_flash_attn.py:4)
+    resolves to the same op objects as the package path."""
+    from kernels import flash_attn as ref_path
+
+    for name in ("_forward", "_backward", "flash_attn", "flash_attn_fwd", "flash_attn_bwd"):
+        assert getattr(ref_path, name) is getattr(fa, name)
+
+
+def test_fused_prologue_needs_one_eps(monkeypatch):
+    """The fused q/k prologue takes one eps; with q_norm.eps != k_norm.eps the block runs
+    the eager norm lines instead (the fused op is never called)."""
+    from tinytrain_amd import attention as att
+
+    def fused_must_not_run(*a, **k):
+        raise AssertionError("fused prologue used with two different eps")
+
+    monkeypatch.setattr(att, "qk_norm_rope", fused_must_not_run)
+    monkeypatch.setattr(att, "causal_attention",
+                        lambda q, k, v, impl, gqa: causal_attention(q, k, v, "sdpa", gqa))
+    blk = att.Attention(64, 4, 2, 16, eps=1e-6)
+    blk.attn_impl, blk.fused_prologue = "hip", True
+    blk.k_norm.eps = 1e-5
+    cos, sin = att.precompute_rope(16, 8, 10000.0)
+    out = blk(torch.randn(1, 8, 64), cos, sin)
+    assert out.shape == (1, 8, 64)
+
+
 def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libttfa.so")

@@ -110,3 +110,43 @@ def test_varlen_autograd_and_opcheck():
                           test_utils=("test_schema", "test_faketensor"))
     torch.library.opcheck(flash_attn_varlen_bwd, (q, k, v, o2, do, M, cu, 200),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_sequence_longer_than_max_seqlen(D):
+    """A sequence longer than max_seqlen is processed as its first max_seqlen tokens by
+    all three kernels: those rows of o, lse, dq, dk, dv are bitwise the batched result on
+    the truncated sequence, and its later rows stay unwritten (NaN poison survives)."""
+    import math
+
+    from tinytrain_amd import _lib
+
+    lens, max_seqlen, Hq, Hkv = [300, 100], 200, 4, 2
+    announce(f"varlen understated max_seqlen lens={lens} max_seqlen={max_seqlen} D={D}")
+    q, k, v, do, cu = (t.to(DEV) for t in _inputs(lens, Hq, Hkv, D, seed=4))
+    total = sum(lens)
+    nan = float("nan")
+    o, dq = torch.full_like(q, nan), torch.full_like(q, nan)
+    dk, dv = torch.full_like(k, nan), torch.full_like(v, nan)
+    M = torch.full((Hq, total), nan, device=DEV)
+    delta = torch.full((Hq, total), nan, device=DEV)
+    lib, s, sc = _lib.load(), torch.cuda.current_stream().cuda_stream, 1.0 / math.sqrt(D)
+    _lib.check(lib.ttfa_varlen_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   M.data_ptr(), cu.data_ptr(), len(lens), total, max_seqlen,
+                                   Hq, Hkv, D, _lib.TTFA_BF16, sc, s))
+    _lib.check(lib.ttfa_varlen_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                   do.data_ptr(), M.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                   dk.data_ptr(), dv.data_ptr(), cu.data_ptr(), len(lens), total,
+                                   max_seqlen, Hq, Hkv, D, _lib.TTFA_BF16, sc, s))
+    torch.cuda.synchronize()
+    for c0, n in ((0, max_seqlen), (lens[0], lens[1])):  # written rows of each sequence
+        sl = lambda t: t[:, c0:c0 + n].unsqueeze(0).contiguous()
+        o1, M1 = _forward(sl(q), sl(k), sl(v))
+        dq1, dk1, dv1 = _backward(sl(q), sl(k), sl(v), o1, sl(do), M1)
+        torch.cuda.synchronize()
+        for name, a, b in (("o", o, o1), ("lse", M, M1), ("dq", dq, dq1), ("dk", dk, dk1),
+                           ("dv", dv, dv1)):
+            assert torch.equal(a[:, c0:c0 + n], b[0]), f"{name} rows [{c0}, {c0 + n}) differ"
+    for name, t in (("o", o), ("lse", M), ("dq", dq), ("dk", dk), ("dv", dv)):
+        assert torch.isnan(t[:, max_seqlen:lens[0]].float()).all(), \
+            f"{name}: rows past max_seqlen of the long sequence were written"

@@ -100,7 +100,9 @@ class Attention(nn.Module):
         q = self.q_proj(x).view(B, T, H, dh)
         k = self.k_proj(x).view(B, T, H_kv, dh)
         v = self.v_proj(x).view(B, T, H_kv, dh)
-        if self.fused_prologue and self.attn_impl == "hip":
+        # The fused op takes one eps for both norms; with different eps the eager lines
+        # below run instead (the reference builds both from config.rms_norm_eps, model.py:70-71).
+        if self.fused_prologue and self.attn_impl == "hip" and self.q_norm.eps == self.k_norm.eps:
             # norm + RoPE + [B, H, T, D] layout in one HIP op (replaces the next 4 lines)
             q, k, v = qk_norm_rope(q, k, v, self.q_norm.weight, self.k_norm.weight, cos, sin,
                                    self.q_norm.eps)

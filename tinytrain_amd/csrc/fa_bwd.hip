@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, const int *__restrict__ cu_seqlens,
-    int n_seq, int total, int Hq, int Hkv, float scale_log2, float scale) {
+    int n_seq, int total, int max_seqlen, int Hq, int Hkv, float scale_log2, float scale) {
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
   using P = DqTile<D>;
   const int per_rank = n_seq * Hq;
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
   const int s = rem / Hq, h = rem - s * Hq;
   const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
   if (c0 < 0 || c1 < c0 || c1 > total) return;
-  const int T = c1 - c0;
+  const int T = min(c1 - c0, max_seqlen);  // the forward's clamp
   const int n_tiles = (T + P::BM - 1) / P::BM;
   if (rank >= n_tiles) return;
   const int qt = n_tiles - 1 - rank;
@@ -529,8 +529,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV,
-    const int *__restrict__ cu_seqlens, int n_seq, int total, int Hq, int Hkv, float scale_log2,
-    float scale) {
+    const int *__restrict__ cu_seqlens, int n_seq, int total, int max_seqlen, int Hq, int Hkv,
+    float scale_log2, float scale) {
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];
   using P = DkvTile<D>;
   const int per_rank = n_seq * Hkv;
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
   const int s = rem / Hkv, hk = rem - s * Hkv;
   const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
   if (c0 < 0 || c1 < c0 || c1 > total) return;
-  const int T = c1 - c0;
+  const int T = min(c1 - c0, max_seqlen);  // the forward's clamp
   if (kt >= (T + P::BNK - 1) / P::BNK) return;
   const int G = Hq / Hkv;
   const int64_t hs = (int64_t)total * D, kvb = (int64_t)hk * hs + (int64_t)c0 * D;
@@ -620,7 +620,8 @@ static hipError_t launch_dq_varlen(const void *q, const void *k, const void *v, 
   const dim3 grid((unsigned)((int64_t)max_tiles * n_seq * Hq)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
-                                     cu_seqlens, n_seq, total, Hq, Hkv, scale * kLog2e, scale);
+                                     cu_seqlens, n_seq, total, max_seqlen, Hq, Hkv, scale * kLog2e,
+                                     scale);
   return hipGetLastError();
 }
 
@@ -640,7 +641,8 @@ static hipError_t launch_dkdv_varlen(const void *q, const void *k, const void *v
   const dim3 grid((unsigned)((int64_t)max_ktiles * n_seq * Hkv)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)dout, lse, delta, (bf16 *)dk, (bf16 *)dv,
-                                     cu_seqlens, n_seq, total, Hq, Hkv, scale * kLog2e, scale);
+                                     cu_seqlens, n_seq, total, max_seqlen, Hq, Hkv, scale * kLog2e,
+                                     scale);
   return hipGetLastError();
 }
 

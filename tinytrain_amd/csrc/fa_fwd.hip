@@ -271,7 +271,7 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void fa_fwd_varlen_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     bf16 *__restrict__ O, float *__restrict__ LSE, const int *__restrict__ cu_seqlens,
-    int n_seq, int total, int Hq, int Hkv, int max_tiles, float scale_log2) {
+    int n_seq, int total, int Hq, int Hkv, int max_seqlen, float scale_log2) {
   using P = FwdTile<D>;
   __shared__ __attribute__((aligned(16))) bf16 lds[2][2][P::BN * D];
   const int per_rank = n_seq * Hq;
@@ -279,7 +279,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_varlen_bf16_kernel(
   const int s = rem / Hq, h = rem - s * Hq;
   const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
   if (c0 < 0 || c1 < c0 || c1 > total) return;
-  const int T = c1 - c0;
+  // A sequence longer than max_seqlen is processed as its first max_seqlen tokens (the
+  // same clamp in all three varlen kernels): those rows are exact, later rows unwritten.
+  const int T = min(c1 - c0, max_seqlen);
+  const int max_tiles = (max_seqlen + P::BM - 1) / P::BM;
   const int n_tiles = (T + P::BM - 1) / P::BM;
   if (rank >= n_tiles) return;
   const int qt = n_tiles - 1 - rank;
@@ -316,7 +319,7 @@ hipError_t launch_fwd_varlen_bf16(const void *q, const void *k, const void *v, v
   const float sl2 = scale * kLog2e;
   auto go = [&](auto kern) {
     kern<<<grid, block, 0, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
-                                     (bf16 *)o, lse, cu_seqlens, n_seq, total, Hq, Hkv, max_tiles,
+                                     (bf16 *)o, lse, cu_seqlens, n_seq, total, Hq, Hkv, max_seqlen,
                                      sl2);
     return hipGetLastError();
   };
