@@ -7,7 +7,8 @@
  * device pointers, sizes and a hipStream_t passed as void*; no torch types appear
  * in the signatures.  The caller owns all memory.  The library allocates nothing,
  * never synchronises the stream, keeps no state between calls and may be called
- * from several host threads at once.
+ * from several host threads at once; the one exception is ttfa_bwd_static, whose
+ * Delta rows live in a static device array shared by its calls on a GPU.
  *
  * Layout contract (kernels/flash_attn.py:220-232, 246-258):
  *   q, o, dout, dq : [B, Hq,  T, D] contiguous, element type `dtype`
@@ -34,7 +35,7 @@
 extern "C" {
 #endif
 
-#define TTFA_ABI_VERSION 4
+#define TTFA_ABI_VERSION 5
 
 enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
 
@@ -49,6 +50,7 @@ enum ttfa_status {
   TTFA_E_SCALE = -7,       /* scale is not finite and positive                   */
   TTFA_E_EPS = -8,         /* eps is not in [0, 1)                               */
   TTFA_E_QROWS = -9,       /* decode: (Hq / Hkv) * Tq > 32                       */
+  TTFA_E_SCRATCH = -10,    /* ttfa_bwd_static: B * Hq * T > TTFA_BWD_STATIC_MAX_ROWS */
 };
 
 /* Library ABI version (TTFA_ABI_VERSION of the build). No reference counterpart. */
@@ -78,6 +80,27 @@ int ttfa_bwd(const void *q, const void *k, const void *v, const void *o,
              const void *dout, const float *lse, float *delta_ws, void *dq,
              void *dk, void *dv, int B, int Hq, int Hkv, int T, int D, int dtype,
              float scale, void *hip_stream);
+
+/*
+ * ttfa_bwd without the delta_ws argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Delta (rowsum(o * dout), B * Hq * T fp32 values) goes
+ * to a library-owned static device array of TTFA_BWD_STATIC_MAX_ROWS floats (4 MiB), one
+ * copy per GPU, held until the process ends; the call allocates nothing and frees nothing.
+ * Same kernels, arguments and results (bitwise) as ttfa_bwd.
+ *   - B * Hq * T > TTFA_BWD_STATIC_MAX_ROWS returns TTFA_E_SCRATCH (before any HIP call).
+ *   - The first call on a device resolves the array's address there (hipGetSymbolAddress,
+ *     cached per device); make that first call outside stream capture.
+ *   - Every call writes all the Delta rows it reads, so no state carries over between
+ *     calls, but calls that overlap in time on one GPU (several streams or host threads)
+ *     share the array and race: serialise them.
+ */
+#define TTFA_BWD_STATIC_MAX_ROWS (1 << 20)
+
+int ttfa_bwd_static(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, void *dq, void *dk, void *dv,
+                    int B, int Hq, int Hkv, int T, int D, int dtype, float scale,
+                    void *hip_stream);
 
 /*
  * The two launches ttfa_bwd is made of, exported separately so a caller (or a

@@ -15,15 +15,16 @@ LIB_PATH = _PKG / "libttfa.so"
 
 TTFA_BF16 = 0
 TTFA_F32 = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Negative status codes of include/ttfa.h.
-E_NULL, E_HEAD_DIM, E_GROUP, E_SEQ, E_ALIGN, E_DTYPE, E_SCALE, E_EPS, E_QROWS = (
-    -1, -2, -3, -4, -5, -6, -7, -8, -9)
+E_NULL, E_HEAD_DIM, E_GROUP, E_SEQ, E_ALIGN, E_DTYPE, E_SCALE, E_EPS, E_QROWS, E_SCRATCH = (
+    -1, -2, -3, -4, -5, -6, -7, -8, -9, -10)
+BWD_STATIC_MAX_ROWS = 1 << 20  # TTFA_BWD_STATIC_MAX_ROWS
 EXPORTED = ("ttfa_abi_version", "ttfa_strerror", "ttfa_fwd", "ttfa_bwd", "ttfa_bwd_dq",
             "ttfa_bwd_dkdv", "ttfa_varlen_fwd", "ttfa_varlen_bwd", "ttfa_decode_workspace_bytes",
             "ttfa_decode_fwd", "ttfa_qk_prologue_fwd",
-            "ttfa_qk_prologue_workspace_bytes", "ttfa_qk_prologue_bwd")
+            "ttfa_qk_prologue_workspace_bytes", "ttfa_qk_prologue_bwd", "ttfa_bwd_static")
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -56,6 +57,7 @@ _SIGS = {
     "ttfa_qk_prologue_fwd": ([_vp] * 12 + [_i] * 5 + [_f, _vp], _i),
     "ttfa_qk_prologue_workspace_bytes": ([_i] * 5, ctypes.c_longlong),
     "ttfa_qk_prologue_bwd": ([_vp] * 17 + [_i] * 5 + [_vp], _i),
+    "ttfa_bwd_static": ([_vp] * 9 + [_i] * 6 + [_f, _vp], _i),
 }
 
 

@@ -6,8 +6,16 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "ttfa.h"
 #include "fa_kernels.h"
+
+// Delta rows of ttfa_bwd_static: a file-scope device array, one copy per GPU the library
+// runs on, held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address): it passes the
+// per-device address hipGetSymbolAddress returns (static_scratch_ptr below).
+static __device__ __align__(256) float scratch[TTFA_BWD_STATIC_MAX_ROWS];
 
 namespace {
 
@@ -55,6 +63,28 @@ int check_decode(int B, int Hq, int Hkv, int Tq, int Lmax, int D, int dtype, flo
   return TTFA_OK;
 }
 
+// Device address of `scratch` on the current device, resolved once per device (the first
+// ttfa_bwd_static call on it) and cached; *out stays null on failure.
+hipError_t static_scratch_ptr(float **out) {
+  static std::atomic<uintptr_t> addr[64];  // by device ordinal, 0 = not resolved yet
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  uintptr_t a = addr[dev].load(std::memory_order_acquire);
+  if (a == 0) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    a = reinterpret_cast<uintptr_t>(ptr);
+    addr[dev].store(a, std::memory_order_release);
+  }
+  *out = reinterpret_cast<float *>(a);
+  return hipSuccess;
+}
+
 int check_ptrs(const void *const *ptrs, int n) {
   for (int i = 0; i < n; ++i)
     if (ptrs[i] == nullptr) return TTFA_E_NULL;
@@ -81,6 +111,8 @@ const char *ttfa_strerror(int code) {
     case TTFA_E_SCALE: return "ttfa: scale must be finite and > 0";
     case TTFA_E_EPS: return "ttfa: eps must be in [0, 1)";
     case TTFA_E_QROWS: return "ttfa: decode needs (Hq / Hkv) * Tq <= 32 query rows per KV head";
+    case TTFA_E_SCRATCH:
+      return "ttfa: ttfa_bwd_static needs B * Hq * T <= TTFA_BWD_STATIC_MAX_ROWS (1048576)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
@@ -191,6 +223,23 @@ int ttfa_bwd(const void *q, const void *k, const void *v, const void *o, const v
   if (rc) return rc;
   return ttfa_bwd_dkdv(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
                        hip_stream);
+}
+
+int ttfa_bwd_static(const void *q, const void *k, const void *v, const void *o,
+                    const void *dout, const float *lse, void *dq, void *dk, void *dv, int B,
+                    int Hq, int Hkv, int T, int D, int dtype, float scale, void *hip_stream) {
+  int rc = check_common(B, Hq, Hkv, T, D, dtype, scale);
+  if (rc) return rc;
+  if ((int64_t)B * Hq * T > TTFA_BWD_STATIC_MAX_ROWS) return TTFA_E_SCRATCH;
+  const void *ptrs[] = {q, k, v, o, dout, lse, dq, dk, dv};
+  if ((rc = check_ptrs(ptrs, 9))) return rc;
+  float *delta = nullptr;
+  hipError_t e = static_scratch_ptr(&delta);
+  if (e != hipSuccess) return static_cast<int>(e);
+  // Every call writes all B * Hq * T rows of Delta (dQ pass) before the dK/dV pass reads
+  // them, so nothing left by an earlier call is ever read and nothing needs clearing.
+  return ttfa_bwd(q, k, v, o, dout, lse, delta, dq, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
+                  hip_stream);
 }
 
 }  // extern "C"
