@@ -264,6 +264,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
     }
   };
 
+  // The first K/V tile is in flight while this wave's rows load and Delta is formed:
+  // both wait on one memory round trip.
+  load_tile(0, 0);
   bf16x8 qf[KK], dof[KK];
   float dpart = 0.f;
 #pragma unroll
@@ -285,7 +288,6 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
 #pragma unroll
   for (int r = 0; r < 16; ++r) ndelta[r] = -delta;
 
-  load_tile(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no register load is pending in the loop
   __syncthreads();
 
