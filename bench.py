@@ -2,8 +2,9 @@
 
 One step = forward + backward of the attention op on one batch of the workload:
 ``ttfa_fwd`` then ``ttfa_bwd_dq`` then ``ttfa_bwd_dkdv`` (the three launches
-``ttfa_fwd`` + ``ttfa_bwd`` make), called through the C ABI on preallocated device
-buffers on torch's current stream.  The default workload is C2, the 112M pretrain
+``ttfa_fwd`` + ``ttfa_bwd`` make in bf16), or ``ttfa_fwd`` then ``ttfa_bwd`` for fp32,
+whose backward is one launch, called through the C ABI on preallocated device buffers
+on torch's current stream.  The default workload is C2, the 112M pretrain
 attention shape (B=16, Hq=Hkv=12, T=1024, D=64, bf16), the configuration the headline
 metric is quoted on.
 
@@ -805,22 +806,36 @@ def main() -> int:
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
 
+    # fp32: ttfa_bwd is a single launch (both passes), timed as one kernel "bwd".
+    one_launch_bwd = cfg.dtype == torch.float32
+    kernel_names = ("fwd", "bwd") if one_launch_bwd else ("fwd", "bwd_dq", "bwd_dkdv")
+
+    launch_sp = [sp]  # the stream the launches go to (a capture stream while capturing)
+
     def launch(s, ev=None):
         q, k, v, do, o, lse, delta, dq, dk, dv = s
         if ev is not None:
             ev[0].record(stream)
         _lib.check(lib.ttfa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                                lse.data_ptr(), B, Hq, Hkv, T, D, dt_code, scale, sp))
+                                lse.data_ptr(), B, Hq, Hkv, T, D, dt_code, scale, launch_sp[0]))
         if ev is not None:
             ev[1].record(stream)
+        if one_launch_bwd:
+            _lib.check(lib.ttfa_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                    do.data_ptr(), lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                    dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, T, D, dt_code, scale,
+                                    launch_sp[0]))
+            if ev is not None:
+                ev[2].record(stream)
+            return
         _lib.check(lib.ttfa_bwd_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                                    do.data_ptr(), lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-                                   B, Hq, Hkv, T, D, dt_code, scale, sp))
+                                   B, Hq, Hkv, T, D, dt_code, scale, launch_sp[0]))
         if ev is not None:
             ev[2].record(stream)
         _lib.check(lib.ttfa_bwd_dkdv(q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
                                      lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                     B, Hq, Hkv, T, D, dt_code, scale, sp))
+                                     B, Hq, Hkv, T, D, dt_code, scale, launch_sp[0]))
         if ev is not None:
             ev[3].record(stream)
 
@@ -844,18 +859,17 @@ def main() -> int:
 
     # Per-kernel breakdown: K more steps on the same rotation, with timing-only HIP events
     # on the launch stream between the three launches of every step.
-    evs = [[HipTimingEvent() for _ in range(4)] for _ in range(K)]
+    evs = [[HipTimingEvent() for _ in range(len(kernel_names) + 1)] for _ in range(K)]
     torch.cuda.synchronize()
     for i in range(K):
         launch(sets[i % nsets], evs[i])
     torch.cuda.synchronize()
 
     def per_kernel(evlist):
-        kms = {"fwd": [], "bwd_dq": [], "bwd_dkdv": []}
+        kms = {n: [] for n in kernel_names}
         for ev in evlist:
-            kms["fwd"].append(ev[0].elapsed_time(ev[1]))
-            kms["bwd_dq"].append(ev[1].elapsed_time(ev[2]))
-            kms["bwd_dkdv"].append(ev[2].elapsed_time(ev[3]))
+            for i, n in enumerate(kernel_names):
+                kms[n].append(ev[i].elapsed_time(ev[i + 1]))
         return kms
 
     kms = per_kernel(evs)
@@ -884,22 +898,56 @@ def main() -> int:
     hot = {n: statistics.median(x) for n, x in per_kernel(evh).items()} if Kh else None
     gemm = _gemm_reference(dev) if cfg.dtype == torch.bfloat16 and not args.no_extras else None
 
+    # Graph replay (outside the timed region above): the same launches, one step per
+    # input set over up to 8 sets, captured once in a HIP graph and replayed, so the host
+    # issues one graph launch instead of one call per kernel.  Where the kernels are
+    # shorter than the host's per-call cost (C1), this is the GPU-side step time.
+    graph_ms = None
+    if not args.no_extras:
+        gsets = min(nsets, 8)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):  # warm-up off the default stream, as capture wants
+            launch_sp[0] = side.cuda_stream
+            for i in range(gsets):
+                launch(sets[i])
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launch_sp[0] = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(gsets):
+                launch(sets[i])
+        launch_sp[0] = sp
+        reps = max(1, K // gsets)
+        for _ in range(2):
+            graph.replay()
+        gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        gs.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        ge.record(stream)
+        torch.cuda.synchronize()
+        graph_ms = gs.elapsed_time(ge) / (reps * gsets)
+
     fwd_f = cfg.fwd_flop()
     peak = PEAK_BF16_TFLOPS if cfg.dtype == torch.bfloat16 else PEAK_F32_TFLOPS
     step_tflops = 3.5 * fwd_f / (ms_step * 1e-3) / 1e12
     fwd_tflops = fwd_f / (avg["fwd"] * 1e-3) / 1e12
-    bwd_ms = avg["bwd_dq"] + avg["bwd_dkdv"]
+    bwd_of = lambda d: d["bwd"] if one_launch_bwd else d["bwd_dq"] + d["bwd_dkdv"]
+    bwd_ms = bwd_of(avg)
     bwd_tflops = 2.5 * fwd_f / (bwd_ms * 1e-3) / 1e12
 
     # Dominant kernel: per causal (query row, key) pair a kernel's MFMA work is 2*D
     # FLOPs per matmul it needs for its outputs: fwd 2 (S, O), dQ pass 3 (S, dP, dQ),
-    # dK/dV pass 4 (S, dP, dV, dK); pairs = B*Hq*T^2/2.
-    n_mm = {"fwd": 2, "bwd_dq": 3, "bwd_dkdv": 4}
+    # dK/dV pass 4 (S, dP, dV, dK), one-launch fp32 backward 7; pairs = B*Hq*T^2/2.
+    n_mm = {"fwd": 2, "bwd_dq": 3, "bwd_dkdv": 4, "bwd": 7}
     dom = max(avg, key=avg.get)
     kern_flop = n_mm[dom] * fwd_f / 2
     achieved = kern_flop / (avg[dom] * 1e-3) / 1e12
     kernel_symbol = {"fwd": "fa_fwd_bf16_kernel", "bwd_dq": "fa_bwd_dq_bf16_kernel",
-                     "bwd_dkdv": "fa_bwd_dkdv_bf16_kernel"}[dom]
+                     "bwd_dkdv": "fa_bwd_dkdv_bf16_kernel", "bwd": "fa_bwd_f32_kernel"}[dom]
     if cfg.dtype == torch.float32:
         kernel_symbol = kernel_symbol.replace("bf16", "f32")
     kernel_symbol += f"<{D}>"
@@ -927,8 +975,8 @@ def main() -> int:
                     "frac": round(fwd_tflops / peak, 4)},
             "bwd": {"ms": round(bwd_ms, 5), "tflops": round(bwd_tflops, 2),
                     "frac": round(bwd_tflops / peak, 4)},
-            "bwd_dq_ms": round(avg["bwd_dq"], 5),
-            "bwd_dkdv_ms": round(avg["bwd_dkdv"], 5),
+            **({} if one_launch_bwd else {"bwd_dq_ms": round(avg["bwd_dq"], 5),
+                                          "bwd_dkdv_ms": round(avg["bwd_dkdv"], 5)}),
             "median_ms": {n: round(x, 5) for n, x in med.items()},
             "timing": "per-kernel times from a second run of K steps right after the timed "
                       "region, timing-only HIP events (hipEventDisableSystemFence) between "
@@ -942,7 +990,13 @@ def main() -> int:
             "fwd_bwd_tflops": round(3.5 * fwd_f / (hot_step_ms * 1e-3) / 1e12, 2),
             "median_ms": {n: round(x, 5) for n, x in hot.items()},
             "fwd_tflops": round(fwd_f / (hot["fwd"] * 1e-3) / 1e12, 2),
-            "bwd_tflops": round(2.5 * fwd_f / ((hot["bwd_dq"] + hot["bwd_dkdv"]) * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(2.5 * fwd_f / (bwd_of(hot) * 1e-3) / 1e12, 2),
+        },
+        "graph_replay": None if graph_ms is None else {
+            "note": "the same launches captured in one HIP graph (one step per input set, "
+                    "up to 8 sets) and replayed: the step without per-call host overhead",
+            "ms_per_step": round(graph_ms, 5),
+            "fwd_bwd_tflops": round(3.5 * fwd_f / (graph_ms * 1e-3) / 1e12, 2),
         },
         "roofline": {
             "bound": "mfma",

@@ -105,7 +105,8 @@ int ttfa_bwd_static(const void *q, const void *k, const void *v, const void *o,
 /*
  * The two launches ttfa_bwd is made of, exported separately so a caller (or a
  * profiler) can run or time each pass on its own.  ttfa_bwd == ttfa_bwd_dq then
- * ttfa_bwd_dkdv on the same stream.
+ * ttfa_bwd_dkdv on the same stream, bitwise.  (For fp32, ttfa_bwd runs both passes as
+ * one launch whose dK/dV workgroups form Delta themselves, with the same results.)
  *
  * ttfa_bwd_dq: writes delta_ws = rowsum(o * dout) and dq.
  *   Replaces bwd_preprocess + bwd_dq_kernel (kernels/flash_attn.py:70-90, :162-217)

@@ -240,6 +240,38 @@ def test_every_output_written(T, D, dtype):
         assert torch.isfinite(t.float()).all(), f"{nm} has unwritten (NaN) elements"
 
 
+@pytest.mark.parametrize("B, H, H_kv, T, D", [(2, 4, 2, 77, 64), (1, 6, 3, 200, 128),
+                                               (2, 4, 4, 256, 64)])
+def test_fp32_one_launch_backward_matches_two_passes(B, H, H_kv, T, D):
+    """fp32 ttfa_bwd is one launch (its dK/dV part forms Delta itself); it must equal
+    ttfa_bwd_dq then ttfa_bwd_dkdv bit for bit."""
+    announce(f"fp32 fused backward vs two passes B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    lib = _lib.load()
+    q, k, v, do = (t.to(DEV) for t in make_custom(B, H, H_kv, T, D, torch.float32, seed=5))
+    s = torch.cuda.current_stream().cuda_stream
+    sc, f32 = 1.0 / math.sqrt(D), _lib.TTFA_F32
+    o, M = torch.empty_like(q), torch.empty((B, H, T), device=DEV)
+    _lib.check(lib.ttfa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), M.data_ptr(),
+                            B, H, H_kv, T, D, f32, sc, s))
+    nan = float("nan")
+    outs = []
+    for fused in (True, False):
+        delta = torch.full((B * H, T), nan, device=DEV)
+        dq, dk, dv = torch.full_like(q, nan), torch.full_like(k, nan), torch.full_like(v, nan)
+        P = [t.data_ptr() for t in (q, k, v, o, do, M, delta, dq, dk, dv)]
+        if fused:
+            _lib.check(lib.ttfa_bwd(*P, B, H, H_kv, T, D, f32, sc, s))
+        else:
+            _lib.check(lib.ttfa_bwd_dq(*P[:8], B, H, H_kv, T, D, f32, sc, s))
+            _lib.check(lib.ttfa_bwd_dkdv(P[0], P[1], P[2], P[4], P[5], P[6], P[8], P[9],
+                                         B, H, H_kv, T, D, f32, sc, s))
+        torch.cuda.synchronize()
+        outs.append((delta, dq, dk, dv))
+    for nm, a, b in zip(("delta", "dq", "dk", "dv"), *outs):
+        assert torch.isfinite(a).all(), f"{nm}: unwritten elements"
+        assert torch.equal(a, b), f"{nm}: one-launch and two-pass results differ"
+
+
 def test_deterministic():
     announce("determinism C3-shaped, B=4")
     q, k, v, do, _ = make_inputs(CONFIGS["C3"], seed=3, batch=4)

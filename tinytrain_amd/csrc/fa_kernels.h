@@ -52,5 +52,10 @@ hipError_t launch_bwd_dkdv_f32(const void *q, const void *k, const void *v, cons
                                const float *lse, const float *delta, void *dk, void *dv,
                                int B, int Hq, int Hkv, int T, int D, float scale,
                                hipStream_t stream);
+// Both fp32 backward passes as one launch (same results, bitwise, as dq then dkdv).
+hipError_t launch_bwd_f32(const void *q, const void *k, const void *v, const void *o,
+                          const void *dout, const float *lse, float *delta, void *dq, void *dk,
+                          void *dv, int B, int Hq, int Hkv, int T, int D, float scale,
+                          hipStream_t stream);
 
 }  // namespace ttfa

@@ -219,6 +219,10 @@ int ttfa_bwd(const void *q, const void *k, const void *v, const void *o, const v
   if (rc) return rc;
   const void *ptrs[] = {q, k, v, o, dout, lse, delta_ws, dq, dk, dv};
   if ((rc = check_ptrs(ptrs, 10))) return rc;
+  if (dtype == TTFA_F32)
+    return static_cast<int>(ttfa::launch_bwd_f32(q, k, v, o, dout, lse, delta_ws, dq, dk, dv, B,
+                                                 Hq, Hkv, T, D, scale,
+                                                 static_cast<hipStream_t>(hip_stream)));
   rc = ttfa_bwd_dq(q, k, v, o, dout, lse, delta_ws, dq, B, Hq, Hkv, T, D, dtype, scale, hip_stream);
   if (rc) return rc;
   return ttfa_bwd_dkdv(q, k, v, dout, lse, delta_ws, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
