@@ -290,6 +290,103 @@ def _measure_sq(config: str, out: Path) -> int:
     return 0
 
 
+# bench.py's symbol stems -> the key of its per-kernel event average in the JSON line
+_EVENT_KEYS = (("fa_fwd_", ("passes", "fwd", "ms")), ("fa_bwd_dq_", ("passes", "bwd_dq_ms")),
+               ("fa_bwd_dkdv_", ("passes", "bwd_dkdv_ms")), ("fa_bwd_f32_", ("passes", "bwd", "ms")))
+
+
+def _measure_kernels(config: str, out: Path) -> int:
+    """rocprofv3 --kernel-trace --stats over one default bench run of ``config`` (a child
+    process): rocprofv3's per-kernel statistics, and the kernel-trace average over the
+    run's per-kernel breakdown steps next to bench.py's own event average for the same
+    launches."""
+    import csv
+    import statistics
+    import subprocess
+
+    me = str(ROOT / "bench.py")
+    work = ["--config", config, "--cpu-budget", "0"]
+    tmp = Path("/tmp") / f"ttfa_kt_{os.getpid()}"
+    tmp.mkdir(parents=True, exist_ok=True)
+    full = ["rocprofv3", "--kernel-trace", "--stats", "-d", str(tmp), "-o", "run",
+            "--output-format", "csv", "--", sys.executable, me, *work]
+    print("[kernels] " + " ".join(full), file=sys.stderr, flush=True)
+    log_path = tmp / "bench.log"
+    with open(log_path, "w") as log:
+        rc = subprocess.run(full, timeout=900, stdout=log, stderr=subprocess.STDOUT, cwd="/tmp",
+                            env={**os.environ, "TMPDIR": "/tmp"}).returncode
+    line = None
+    for text in open(log_path):
+        if text.startswith("{"):
+            line = json.loads(text)
+    stats = sorted(tmp.rglob("*kernel_stats.csv"))
+    traces = sorted(tmp.rglob("*kernel_trace.csv"))
+    if line is None or not stats or not traces:
+        print(f"[kernels] rocprofv3 exited {rc} without a bench line or its csv files; "
+              f"see {log_path}", file=sys.stderr)
+        return 1
+    steps, warmup = line["steps"], line["warmup"]
+    durs: dict = {}
+    for row in sorted(csv.DictReader(open(traces[0])), key=lambda r: int(r["Start_Timestamp"])):
+        name = row["Kernel_Name"]
+        if "ttfa::" not in name:
+            continue
+        sym = name.split("ttfa::", 1)[1].split("(", 1)[0]
+        durs.setdefault(sym, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    c = line["config"]
+    desc = (f"B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} T={c['T']} D={c['D']} {line['dtype']}")
+    lines = [
+        f"# rocprofv3 kernel-trace statistics, workload {config} ({desc}), 1x MI355X",
+        f"# command: python bench.py --measure-kernels --config {config}",
+        "# which runs: cd /tmp && TMPDIR=/tmp rocprofv3 --kernel-trace --stats -d <out> -o run "
+        f"--output-format csv -- python bench.py {' '.join(work)}",
+        f"# Dispatches per kernel: {warmup} warmup + {steps} timed steps (no event between "
+        f"launches) + {steps} breakdown steps (timing-only HIP events between launches) + "
+        "hot-cache and graph-replay launches.",
+        "# 'Calls'/'AverageNs' below are rocprofv3's own statistics over all of them.",
+        "",
+    ]
+    for row in csv.reader(open(stats[0])):
+        if row[0] == "Name" or "ttfa::" in row[0]:
+            lines.append(",".join(f'"{x}"' if i == 0 else x for i, x in enumerate(row)))
+    lines += [
+        "",
+        f"# Breakdown steps (dispatches {warmup + steps + 1}-{warmup + 2 * steps} of each kernel, "
+        "rotated input sets) from the kernel trace,",
+        "# against bench.py's event averages for the same launches in the same run:",
+        f"{'kernel':36s} {'rocprof avg us':>15s} {'bench events us':>16s}  difference",
+    ]
+    summary = {}
+    for sym, d in durs.items():
+        window = d[warmup + steps:warmup + 2 * steps]
+        keys = next((k for stem, k in _EVENT_KEYS if sym.startswith(stem)), None)
+        if not window or keys is None:
+            continue
+        ev = line
+        for k in keys:
+            ev = ev[k]
+        avg = statistics.mean(window)
+        summary[sym] = {"rocprof_avg_us": round(avg, 3), "bench_event_us": round(ev * 1e3, 3)}
+        lines.append(f"{sym:36s} {avg:15.2f} {ev * 1e3:16.2f}  {100 * (ev * 1e3 / avg - 1):+.1f}%")
+    r = line["roofline"]
+    g = line.get("graph_replay") or {}
+    lines += [
+        "# The events time launch to launch on the stream, so they include the dispatch gap between",
+        "# back-to-back kernels (a few microseconds); rocprofv3 times the kernel alone.",
+        f"# bench.py in this run (under the profiler): value {line['value']} TFLOP/s, ms_per_step "
+        f"{line['ms_per_step']}, graph-replay ms_per_step {g.get('ms_per_step')}, roofline "
+        f"{r['kernel']} achieved {r['achieved']} TFLOP/s ({r['frac']})",
+        "JSON " + json.dumps({"config": config, "kernels": summary, "bench": {
+            k: line[k] for k in ("value", "ms_per_step", "passes", "roofline", "graph_replay")}}),
+    ]
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines), flush=True)
+    if rc != 0:  # rocprofv3 can exit non-zero after the program's complete run
+        print(f"[kernels] rocprofv3 exited {rc} after a complete bench run", file=sys.stderr)
+    return 0
+
+
 def _measure_traffic(config: str, out: Path) -> int:
     """FETCH_SIZE and WRITE_SIZE per dispatch of each attention kernel on ``config``,
     scaled by what the same counters read for a plain 256 MB device copy."""
@@ -733,6 +830,9 @@ def main() -> int:
     ap.add_argument("--measure-sq", action="store_true",
                     help="run two rocprofv3 SQ-counter passes over --config (MFMA busy, VALU, "
                          "LDS bank conflicts) and write profiles/sq_counters_<cfg>.txt")
+    ap.add_argument("--measure-kernels", action="store_true",
+                    help="run bench.py --config under rocprofv3 --kernel-trace --stats and "
+                         "write profiles/fa_kernels_<cfg>_kernel_stats.txt")
     ap.add_argument("--prologue", action="store_true",
                     help="benchmark the fused q/k norm + RoPE + layout op against the eager "
                          "expressions it replaces (prints its own JSON line)")
@@ -761,6 +861,9 @@ def main() -> int:
         return _measure_traffic(args.config, out)
     if args.measure_sq:
         return _measure_sq(args.config, TRAFFIC_DIR / f"sq_counters_{args.config}.txt")
+    if args.measure_kernels:
+        return _measure_kernels(args.config,
+                                TRAFFIC_DIR / f"fa_kernels_{args.config}_kernel_stats.txt")
 
     import torch
 
