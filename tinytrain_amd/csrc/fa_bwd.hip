@@ -74,6 +74,9 @@ __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf
   const int lq = lane & 31, lg = lane >> 5;
 #pragma unroll
   for (int kb = 0; kb < P::KB; ++kb) {
+    // Inside T, a 32-key block after every row of the wave contributes nothing
+    // (wave-uniform: the wave's rows start at qrow - lq).
+    if (MASK && k0 + P::BN <= T && k0 + 32 * kb > qrow - lq + 31) continue;
     f32x16 s, dp;
     {
       bf16x8 kf[P::KK], vf[P::KK];

@@ -210,7 +210,9 @@ __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 // the pair runs first.  When n is odd the middle tile forms a pair of its own.
 //
 // Hardware hands consecutive workgroup ids to the 8 XCDs round-robin (id % 8), and each
-// XCD has its own L2.  When the number of (batch, kv-head) groups is a multiple of 8,
+// XCD has its own L2.  (This holds for a whole MI355X, SPX mode.  The grouping below is
+// a bijection from workgroup ids to items for any XCD count, so another partition mode
+// changes only which L2 serves an item, never the results.)  When the number of (batch, kv-head) groups is a multiple of 8,
 // each group's items (its G query heads x pairs) are placed on one XCD and numbered
 // consecutively there, so the workgroups that read the same K/V run at the same time
 // on the same L2.  Otherwise items are numbered group-major in plain id order.
@@ -285,23 +287,25 @@ inline int sched_items(bool paired, int n_tiles, int B, int H) {
   return (paired ? (n_tiles + 1) / 2 : n_tiles) * B * H;
 }
 
-// Workgroups of kernel KERN resident on the whole device at once: CUs x blocks per CU,
-// from the runtime's occupancy calculator, cached per kernel (one value per process: the
-// supported set-up is one MI355X, and every MI355X gives the same value).
+// Workgroups of kernel KERN resident on the current device at once: CUs x blocks per CU,
+// from the runtime's occupancy calculator, cached per kernel and device (devices 0..63;
+// a higher id is asked every time).  The value only picks the work schedule (pairs or
+// single row tiles), never the results.
 template <auto KERN>
 inline int resident_slots(int block, size_t lds) {
-  static std::atomic<int> cached{0};
-  int v = cached.load(std::memory_order_relaxed);
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  int v = dev >= 0 && dev < 64 ? cached[dev].load(std::memory_order_relaxed) : 0;
   if (v) return v;
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(KERN),
                                                    block, lds) != hipSuccess ||
       cus <= 0 || per_cu <= 0)
     return 1;  // unknown: then pairs are used only when they fill rounds of one slot
   v = cus * per_cu;
-  cached.store(v, std::memory_order_relaxed);
+  if (dev >= 0 && dev < 64) cached[dev].store(v, std::memory_order_relaxed);
   return v;
 }
 
