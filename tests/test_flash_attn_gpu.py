@@ -113,6 +113,8 @@ def test_config_parity(name):
     (1, 1, 1, 1, 128, torch.float32),
     (1, 2, 1, 33, 128, torch.float32),
     (2, 4, 2, 100, 64, torch.float32),
+    (1, 8, 1, 300, 64, torch.float32),     # fp32, G=8: dK/dV items over eight query heads
+    (1, 4, 1, 1000, 128, torch.float32),   # fp32, long rows at D=128
 ])
 def test_edge_shapes(B, H, H_kv, T, D, dtype):
     announce(f"edge B={B} H={H} Hkv={H_kv} T={T} D={D} {dtype}")
