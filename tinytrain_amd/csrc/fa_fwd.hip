@@ -150,38 +150,11 @@ struct FwdHead {
   int T;
 };
 
-// Row tile qt's Q block (128 rows) from global memory into the swizzled LDS block qlds,
-// without registers: two 64-row halves, each loaded like a K tile (lane offsets voff,
-// LDS destinations from the scalar wave index); rows past T read as zero.
-template <int D>
-__device__ __forceinline__ void fwd_load_q(const FwdHead &hd, bf16 *qlds, int qt,
-                                           const uint32_t (&voff)[FwdTile<D>::LOADS], int wave_s) {
-  using P = FwdTile<D>;
-  const uint32_t head_bytes = (uint32_t)hd.T * D * 2;
-#pragma unroll
-  for (int h = 0; h < P::BM / P::BN; ++h) {
-    const int64_t t0 = ((int64_t)qt * P::BM + h * P::BN) * D;
-    const uint32_t left = (uint32_t)t0 * 2 < head_bytes ? head_bytes - (uint32_t)t0 * 2 : 0u;
-    const auto r = make_rsrc(hd.q + t0, left);
-#pragma unroll
-    for (int i = 0; i < P::LOADS; ++i)
-      buf_load16_lds(r, voff[i], qlds + h * P::BN * D + (256 * i + 64 * wave_s) * 8);
-  }
-}
-
 // All 128 query rows of row tile qt of one head: online softmax over its key tiles.
 // Ends with a workgroup barrier, so the caller may reuse the LDS ring right away.
-//
-// QPF (a workgroup with a second row tile): the row tile's Q block comes through the
-// LDS block qlds, and its first K/V tile sits in ring stage s0, both already loaded and
-// visible (the caller's or the previous row tile's doing).  The last key tile's
-// iteration then requests row tile next_qt's Q block and first K/V tile (into stage
-// s0 + n_kv), so the next row tile starts without a memory round trip of its own.
-// Without QPF the Q fragments and the first tile are loaded here (stage 0).
-template <int D, bool QPF = false>
+template <int D>
 __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], const FwdHead &hd,
-                                         int qt, float scale_log2, int work_left, int work_max,
-                                         const bf16 *qlds = nullptr, int s0 = 0, int next_qt = -1) {
+                                         int qt, float scale_log2, int work_left, int work_max) {
   using P = FwdTile<D>;
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   const int T = hd.T;
@@ -221,19 +194,14 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
 
   // Q^T as B operand: lane (lq, lg) slot s of step kk holds Q[qrow][16kk + 8lg + s].
   bf16x8 qf[KK];
-  if constexpr (QPF) {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qf[kk] = lds_read_row8<D>(qlds, wave * 32 + lq, 2 * kk + lg);
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
-    load_tile(0, 0);
-    // Every load issued so far (Q and the first tile) is complete here, so the loop body
-    // never waits on the Q registers behind the next tile's prefetch.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-  }
+  for (int kk = 0; kk < KK; ++kk)
+    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
+  load_tile(0, 0);
+  // Every load issued so far (Q and the first tile) is complete here, so the loop body
+  // never waits on the Q registers behind the next tile's prefetch.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
 
   const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
   // Tiles [0, n_full) are visible to every row of this wave and lie inside T;
@@ -250,16 +218,9 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
   PrioByRemaining prio(work_max);
   for (int j = 0; j < n_kv; ++j) {
     prio.update(work_left - j);
-    if (j + 1 < n_kv) {
-      load_tile(j + 1, (s0 + j + 1) & 1);
-    } else if (QPF && next_qt >= 0 && j > 0) {
-      // The next row tile's first K/V tile and Q block: every wave read its Q fragments
-      // from qlds before the first iteration's barrier, so the block is free.
-      load_tile(0, (s0 + n_kv) & 1);
-      fwd_load_q<D>(hd, const_cast<bf16 *>(qlds), next_qt, voff, wave_s);
-    }
-    const bf16 *Kt = lds[(s0 + j) & 1][0];
-    const bf16 *Vt = lds[(s0 + j) & 1][1];
+    if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
+    const bf16 *Kt = lds[j & 1][0];
+    const bf16 *Vt = lds[j & 1][1];
     if (j < n_full)
       fwd_tile<D, false>(Kt, Vt, qf, oacc, m_t, l_part, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
@@ -268,17 +229,10 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
     __syncthreads();
   }
 
-  if (QPF && next_qt >= 0 && n_kv == 1) {  // no earlier iteration to hide it under
-    load_tile(0, (s0 + 1) & 1);
-    fwd_load_q<D>(hd, const_cast<bf16 *>(qlds), next_qt, voff, wave_s);
-    wait_vm_all();
-    __syncthreads();
-  }
-  // The loop's last barrier freed the stage of the last key tile: each wave stages its O
-  // tile in its own 32*D slice of it for row-contiguous stores.  (The other stage may
-  // hold the next row tile's first K/V tile.)
+  // The loop's last barrier freed the LDS ring: each wave stages its O tile in its own
+  // 32*D slice of it for row-contiguous stores.
   const float l = xhalf_sum(l_part);
-  store_rows<D>(oacc, 1.f / l, &lds[(s0 + n_kv - 1) & 1][0][0] + wave * 32 * D, hd.o, q0, T, lane);
+  store_rows<D>(oacc, 1.f / l, &lds[0][0][0] + wave * 32 * D, hd.o, q0, T, lane);
   if (qrow < T && lg == 0) hd.lse[qrow] = (m_t + __log2f(l)) * kLn2;
   __syncthreads();  // the ring is free again for the caller
 }
@@ -289,12 +243,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
     bf16 *__restrict__ O, float *__restrict__ LSE, int B, int Hq, int Hkv, int T,
     float scale_log2, int paired) {
   using P = FwdTile<D>;
-  // D = 64: the Q blocks go through LDS too (16 KB more; three workgroups per CU still
-  // fit), so that a workgroup's second row tile is prefetched under its first.  At
-  // D = 128 that block would cost the second workgroup per CU.
-  constexpr bool QPF = D == 64;
   __shared__ __attribute__((aligned(16))) bf16 lds[2][2][P::BN * D];  // [stage][K|V]
-  __shared__ __attribute__((aligned(16))) bf16 qlds[QPF ? P::BM * D : 8];
   const int n_tiles = (T + P::BM - 1) / P::BM;
   const WorkPair w = sched_item(paired, blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
   // Key tiles a row tile visits is its work; the priority scales by the largest
@@ -308,36 +257,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
   const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D;
   const FwdHead hd{Q + w.bh * hs, K + kvh * hs, V + kvh * hs, O + w.bh * hs,
                    LSE + (int64_t)w.bh * T, T};
-  if constexpr (QPF) {
-    // First row tile's Q block and first K/V tile (stage 0), then the two row tiles;
-    // the first one's last iteration prefetches the second's.
-    {
-      const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wave_s = wave_id();
-      uint32_t voff[P::LOADS];
-#pragma unroll
-      for (int i = 0; i < P::LOADS; ++i) {
-        const int e = 256 * i + 64 * wave + lane, row = e / P::CH, pc = e % P::CH;
-        voff[i] = (uint32_t)(row * D + swz<D>(row, pc) * 8) * 2;
-      }
-      fwd_load_q<D>(hd, qlds, w.first, voff, wave_s);
-      const uint32_t head_bytes = (uint32_t)T * D * 2;
-      const auto rk = make_rsrc(hd.k, head_bytes), rv = make_rsrc(hd.v, head_bytes);
-#pragma unroll
-      for (int i = 0; i < P::LOADS; ++i) {
-        const int e0 = 256 * i + 64 * wave_s;
-        buf_load16_lds(rk, voff[i], &lds[0][0][e0 * 8]);
-        buf_load16_lds(rv, voff[i], &lds[0][1][e0 * 8]);
-      }
-      wait_vm_all();
-      __syncthreads();
-    }
-    fwd_rows<D, true>(lds, hd, w.first, scale_log2, w1 + w2, wmax, qlds, 0, w.second);
-    if (w.second >= 0)
-      fwd_rows<D, true>(lds, hd, w.second, scale_log2, w2, wmax, qlds, work(w.first) & 1, -1);
-  } else {
-    fwd_rows<D>(lds, hd, w.first, scale_log2, w1 + w2, wmax);
-    if (w.second >= 0) fwd_rows<D>(lds, hd, w.second, scale_log2, w2, wmax);
-  }
+  fwd_rows<D>(lds, hd, w.first, scale_log2, w1 + w2, wmax);
+  if (w.second >= 0) fwd_rows<D>(lds, hd, w.second, scale_log2, w2, wmax);
 }
 
 // Packed variable-length sequences ([H, total, D] per tensor, sequence s at rows
