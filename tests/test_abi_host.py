@@ -94,6 +94,8 @@ CASES = [
     (dict(T=0), _lib.E_SEQ),
     (dict(B=0), _lib.E_SEQ),
     (dict(T=1 << 24), _lib.E_SEQ),          # one head's bytes exceed the 2 GiB window
+    # fp32: one workgroup per 16-row block of every query and KV head, 2^31 of them
+    (dict(dtype=1, D=64, B=1 << 14, Hq=1, Hkv=1, T=1 << 20), _lib.E_SEQ),
     (dict(dtype=2), _lib.E_DTYPE),
     (dict(dtype=-1), _lib.E_DTYPE),
     (dict(scale=0.0), _lib.E_SCALE),

@@ -30,6 +30,9 @@ int check_common(int B, int Hq, int Hkv, int T, int D, int dtype, float scale) {
   if ((int64_t)T * D * esz > (int64_t)0x7fffffff) return TTFA_E_SEQ;
   if ((int64_t)B * Hq > (int64_t)0x7fffffff / 4) return TTFA_E_SEQ;
   if ((int64_t)B * Hq * ((T + 127) / 128) > (int64_t)0x7fffffff) return TTFA_E_SEQ;
+  // fp32 grids: one workgroup per 16-row block of every query and KV head.
+  if (dtype == TTFA_F32 && (int64_t)B * (Hq + Hkv) * ((T + 15) / 16) > (int64_t)0x7fffffff)
+    return TTFA_E_SEQ;
   if (!(scale > 0.f) || !isfinite(scale)) return TTFA_E_SCALE;
   return TTFA_OK;
 }
