@@ -64,6 +64,22 @@ struct DkvTile {
   static constexpr int LDS_BYTES = 2 * 2 * BMQ * D * 2 + 2 * 2 * BMQ * 4;
 };
 
+// S/dP products of the D = 128 dK/dV pass with the accumulator in VGPRs and the K/V
+// operand in AGPRs.  That kernel needs AGPRs (dK/dV), so the builtin gets the AGPR form
+// for all its MFMAs and every S/dP result would cross back to VGPRs (v_accvgpr_read) for
+// the exponentials: 64 copies per item on SIMDs that hold one wave.  The compiler's
+// hazard checks do not see inside inline asm, so the operands must not come from a VALU
+// write just before (here: LDS reads, buffer loads, and the previous product of the
+// same chain), and a chain ends with mfma_vacc_drain before any VALU reads its result.
+__device__ __forceinline__ void mfma32_vacc(f32x16 &acc, bf16x8 a, bf16x8 b_agpr) {
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b_agpr));
+}
+// 24 wait states after a chain of mfma32_vacc, twice what the compiler puts between a
+// product of this shape and a VALU read of its result.
+__device__ __forceinline__ void mfma_vacc_drain(f32x16 &x, f32x16 &y) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(x), "+v"(y));
+}
+
 // One key tile of the dQ pass for one wave, one 32-key block at a time.
 template <int D, bool MASK>
 __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf16x8 (&qf)[D / 16],
@@ -162,12 +178,23 @@ __device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, con
       qa[kk] = lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg);
       da[kk] = lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg);
     }
-    s[nb] = mfma32(qa[0], kf[0], ns);
-    dp[nb] = mfma32(da[0], vf[0], nd);
+    if constexpr (D == 128) {
+      s[nb] = ns;
+      dp[nb] = nd;
 #pragma unroll
-    for (int kk = 1; kk < P::KK; ++kk) {
-      s[nb] = mfma32(qa[kk], kf[kk], s[nb]);
-      dp[nb] = mfma32(da[kk], vf[kk], dp[nb]);
+      for (int kk = 0; kk < P::KK; ++kk) {
+        mfma32_vacc(s[nb], qa[kk], kf[kk]);
+        mfma32_vacc(dp[nb], da[kk], vf[kk]);
+      }
+      mfma_vacc_drain(s[nb], dp[nb]);
+    } else {
+      s[nb] = mfma32(qa[0], kf[0], ns);
+      dp[nb] = mfma32(da[0], vf[0], nd);
+#pragma unroll
+      for (int kk = 1; kk < P::KK; ++kk) {
+        s[nb] = mfma32(qa[kk], kf[kk], s[nb]);
+        dp[nb] = mfma32(da[kk], vf[kk], dp[nb]);
+      }
     }
   }
 #pragma unroll
@@ -412,6 +439,11 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
     const uint32_t off = (uint32_t)(krow * D + 16 * kk + 8 * lg) * 2;
     kf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rk, off));
     vf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rv, off));
+  }
+  if constexpr (D == 128) {
+    // K/V fragments live in AGPRs at D = 128 (operands of the S/dP products there).
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(kf[kk]), "+a"(vf[kk]));
   }
 
   const int n_qt = (T + BMQ - 1) / BMQ;
