@@ -54,8 +54,23 @@ def _compile(src: Path, extra: list[str]) -> Path:
     return obj
 
 
+def _generate() -> None:
+    """Rewrites generated sources whose generator output has changed (the D = 64 dK/dV
+    stage schedule, csrc/gen_dkdv64_asm.py -> csrc/dkdv64_item.inc)."""
+    sys.path.insert(0, str(CSRC))
+    try:
+        import gen_dkdv64_asm as gen
+    finally:
+        sys.path.pop(0)
+    text = gen.render()
+    out = Path(gen.DEFAULT_OUT)
+    if not out.exists() or out.read_text() != text:
+        out.write_text(text)
+
+
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     """Compile all sources and link libttfa.so; returns the library path."""
+    _generate()
     OBJ_DIR.mkdir(exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     extra = list(extra_flags or [])

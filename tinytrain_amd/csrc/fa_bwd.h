@@ -1,0 +1,65 @@
+// Declarations shared by the backward translation units: the dK/dV pass's per-head view,
+// its kernel templates (fa_bwd.hip defines them; the D = 64 specialization of the batched
+// kernel is the hand-scheduled pass in fa_bwd_dkdv64.hip, while packed variable-length
+// sequences at D = 64 keep the generic body) and the dynamic-LDS opt-in.
+#pragma once
+
+#include <atomic>
+
+#include "fa_common.h"
+
+namespace ttfa {
+
+// One KV head's rows (k, v, dk, dv: T rows of D) for one sequence, and the G query heads
+// that read it: query head g's q / dout rows at q + g * head_stride (elements), its lse /
+// delta values at lse + g * row_stride.
+struct DkvHead {
+  const bf16 *k, *v;
+  bf16 *dk, *dv;
+  const bf16 *q, *dout;
+  const float *lse, *delta;
+  int64_t head_stride, row_stride;
+  int G, T;
+};
+
+template <int D>
+__global__ void fa_bwd_dkdv_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                        const bf16 *__restrict__ V, const bf16 *__restrict__ dO,
+                                        const float *__restrict__ LSE,
+                                        const float *__restrict__ Delta, bf16 *__restrict__ dK,
+                                        bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
+                                        float scale_log2, float scale, int paired);
+template <int D>
+__global__ void fa_bwd_dkdv_varlen_bf16_kernel(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE, const float *__restrict__ Delta,
+    bf16 *__restrict__ dK, bf16 *__restrict__ dV, const int *__restrict__ cu_seqlens, int n_seq,
+    int total, int max_seqlen, int Hq, int Hkv, float scale_log2, float scale);
+template <>
+__global__ void fa_bwd_dkdv_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                            const bf16 *__restrict__ V, const bf16 *__restrict__ dO,
+                                            const float *__restrict__ LSE,
+                                            const float *__restrict__ Delta, bf16 *__restrict__ dK,
+                                            bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
+                                            float scale_log2, float scale, int paired);
+// LDS bytes of the D = 64 dK/dV pass: two 128-row stages of Q and dO tiles plus their
+// -LSE/scale and -Delta rows.
+constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
+
+// Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,
+// including launches under stream capture, make no attribute call.
+template <auto KERN>
+static hipError_t allow_lds(size_t bytes) {
+  static std::atomic<uint64_t> done{0};  // bit d: set on device d
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t{1} << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
+
+}  // namespace ttfa

@@ -37,6 +37,7 @@
 // lane, no staging VGPRs), the next tile's loads in flight while the current tile is
 // computed.  Tiles entirely above the diagonal are skipped; only tiles crossing the
 // diagonal or the ragged end of T run the masked body.
+#include "fa_bwd.h"
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -400,18 +401,8 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
 }
 
 // ---------------------------------------------------------------- pass 2: dK, dV
-// One KV head's rows (k, v, dk, dv: T rows of D) for one sequence, and the G query heads
-// that read it: query head g's q / dout rows at q + g * head_stride (elements), its lse /
-// delta values at lse + g * row_stride.
-struct DkvHead {
-  const bf16 *k, *v;
-  bf16 *dk, *dv;
-  const bf16 *q, *dout;
-  const float *lse, *delta;
-  int64_t head_stride, row_stride;
-  int G, T;
-};
-
+// (The batched kernel at D = 64 is the hand-scheduled pass in fa_bwd_dkdv64.hip; this
+// body serves D = 128 and the packed variable-length kernel at both head dims.)
 // dK and dV for the 128 keys of key tile kt of one KV head, reduced over the head's
 // query-head group.  Ends with a workgroup barrier, so the caller may reuse the LDS ring
 // right away.
@@ -539,7 +530,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
 }
 
 template <int D>
-__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_bf16_kernel(
+__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
@@ -586,22 +577,6 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
   dkdv_rows<D>(smem, hd, kt, scale_log2, scale);
 }
 
-// Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,
-// including launches under stream capture, make no attribute call.
-template <auto KERN>
-static hipError_t allow_lds(size_t bytes) {
-  static std::atomic<uint64_t> done{0};  // bit d: set on device d
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t{1} << dev : 0;
-  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
-  e = hipFuncSetAttribute(reinterpret_cast<const void *>(KERN),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
-  return e;
-}
-
 template <int D>
 static hipError_t launch_dq(const void *q, const void *k, const void *v, const void *o,
                             const void *dout, const float *lse, float *delta, void *dq, int B,
@@ -627,7 +602,7 @@ static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const
                               const float *lse, const float *delta, void *dk, void *dv, int B,
                               int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   const int n_ktiles = (T + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
-  constexpr size_t lds = DkvTile<D>::LDS_BYTES;
+  constexpr size_t lds = D == 64 ? kDkv64LdsBytes : DkvTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dkdv_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds<fa_bwd_dkdv_bf16_kernel<D>>(lds);
