@@ -1,4 +1,5 @@
-"""The generated D = 64 dK/dV stage schedule (tinytrain_amd/csrc/dkdv64_item.inc).
+"""The generated D = 64 stage schedules of the backward passes (tinytrain_amd/csrc/
+dkdv64_item.inc for the dK/dV pass, dq64_stage.inc for the dQ pass).
 
 The generator inserts the LDS waits and hazard padding that the compiler does not add
 inside an asm statement.  This test re-checks the emitted text with an independent
@@ -22,23 +23,23 @@ import pytest
 CSRC = Path(__file__).resolve().parent.parent / "tinytrain_amd" / "csrc"
 
 
-def _gen():
+def _gen(name="gen_dkdv64_asm"):
+    import importlib
     sys.path.insert(0, str(CSRC))
     try:
-        import gen_dkdv64_asm as gen
+        return importlib.import_module(name)
     finally:
         sys.path.pop(0)
-    return gen
 
 
-def _variants(text):
+def _variants(text, macro="TTFA_DKDV64_STAGE_ASM", label="dkv"):
     """{name: [instruction lines]} from the generated statement."""
-    body = re.search(r"#define TTFA_DKDV64_STAGE_ASM \\\n(.*?)\n\n", text, re.S).group(1)
+    body = re.search(r"#define " + macro + r" \\\n(.*?)\n\n", text, re.S).group(1)
     lines = [m.group(1) for m in re.finditer(r'"(.*?)\\n"', body)]
     out, cur = {}, "FULL"
     out[cur] = []
     for ln in lines:
-        m = re.match(r"\.Ldkv_(\w+?)_%=:", ln)
+        m = re.match(r"\.L" + label + r"_(\w+?)_%=:", ln)
         if m:
             cur = m.group(1)
             out[cur] = []
@@ -71,11 +72,13 @@ def _decode(ln):
         return "lds", [], _regs(toks[0])
     if op.startswith("v_mfma"):
         dst, a, b, c = toks[:4]
-        return "mfma", _regs(a) + _regs(b) + _regs(c), _regs(dst)
+        return "mfma", _regs(a) + _regs(b) + (_regs(c) if c != "0" else []), _regs(dst)
     if op == "v_exp_f32":
         return "trans", _regs(toks[1]), _regs(toks[0])
     if op.startswith("v_cmp"):
         return "valu", [r for t in toks[1:] for r in _regs(t)], ["vcc"]
+    if op == "v_mov_b32":
+        return "valu", [], _regs(toks[0])
     if op.startswith("v_"):
         reads = [r for t in toks[1:] for r in _regs(t)]
         if op.startswith("v_cndmask"):
@@ -159,3 +162,26 @@ def test_checker_catches_a_dropped_wait_or_nop():
         i = next(k for k, ln in enumerate(lines) if ln.startswith(prefix) and k > 2)
         with pytest.raises(AssertionError):
             _check_stream(lines[:i] + lines[i + 1:])
+
+
+def test_dq_committed_file_is_the_generator_output():
+    gen = _gen("gen_dq64_asm")
+    assert (CSRC / "dq64_stage.inc").read_text() == gen.render(), \
+        "dq64_stage.inc is stale: run python tinytrain_amd/csrc/gen_dq64_asm.py"
+
+
+@pytest.mark.parametrize("name", ["FULL", "DIAG0", "DIAG1", "DIAG2", "DIAG3", "RAGGED"])
+def test_dq_stream_rules_and_counts(name):
+    var = _variants(_gen("gen_dq64_asm").render(), "TTFA_DQ64_STAGE_ASM", "dq")
+    assert set(var) == {"FULL", "DIAG0", "DIAG1", "DIAG2", "DIAG3", "RAGGED"}
+    lines = var[name]
+    _check_stream(lines)
+    n_blocks = int(name[-1]) + 1 if name.startswith("DIAG") else 4
+    count = lambda p: sum(1 for ln in lines if ln.startswith(p))
+    assert count("v_mfma") == 12 * n_blocks           # S^T, dP^T: 8; dQ^T: 4 per block
+    assert count("ds_read") == 16 * n_blocks          # 8 row fragments, 8 transposed halves
+    assert count("v_exp_f32") == 16 * n_blocks
+    assert count("v_mov_b32") == 16 * n_blocks        # dP^T starts at -Delta
+    masked = {"FULL": 0, "RAGGED": 4}.get(name, 1)
+    assert count("v_cmp_gt_i32") == 16 * masked
+    assert count("v_cvt_pk_bf16_f32") == 8 * n_blocks

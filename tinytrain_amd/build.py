@@ -55,17 +55,20 @@ def _compile(src: Path, extra: list[str]) -> Path:
 
 
 def _generate() -> None:
-    """Rewrites generated sources whose generator output has changed (the D = 64 dK/dV
-    stage schedule, csrc/gen_dkdv64_asm.py -> csrc/dkdv64_item.inc)."""
+    """Rewrites generated sources whose generator output has changed: the D = 64 stage
+    schedules of the dK/dV pass (csrc/gen_dkdv64_asm.py -> csrc/dkdv64_item.inc) and of
+    the dQ pass (csrc/gen_dq64_asm.py -> csrc/dq64_stage.inc)."""
+    import importlib
     sys.path.insert(0, str(CSRC))
     try:
-        import gen_dkdv64_asm as gen
+        gens = [importlib.import_module(m) for m in ("gen_dkdv64_asm", "gen_dq64_asm")]
     finally:
         sys.path.pop(0)
-    text = gen.render()
-    out = Path(gen.DEFAULT_OUT)
-    if not out.exists() or out.read_text() != text:
-        out.write_text(text)
+    for gen in gens:
+        text = gen.render()
+        out = Path(gen.DEFAULT_OUT)
+        if not out.exists() or out.read_text() != text:
+            out.write_text(text)
 
 
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:

@@ -1,7 +1,8 @@
 // Declarations shared by the backward translation units: the dK/dV pass's per-head view,
-// its kernel templates (fa_bwd.hip defines them; the D = 64 specialization of the batched
-// kernel is the hand-scheduled pass in fa_bwd_dkdv64.hip, while packed variable-length
-// sequences at D = 64 keep the generic body) and the dynamic-LDS opt-in.
+// the kernel templates (fa_bwd.hip defines them; the D = 64 specializations of the batched
+// kernels are the hand-scheduled passes in fa_bwd_dq64.hip and fa_bwd_dkdv64.hip, while
+// packed variable-length sequences at D = 64 keep the generic bodies), the staged-tile
+// helpers of those passes and the dynamic-LDS opt-in.
 #pragma once
 
 #include <atomic>
@@ -22,6 +23,38 @@ struct DkvHead {
   int G, T;
 };
 
+// LDS byte address of a pointer into the workgroup's shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const TTFA_LDS void *)p;
+}
+
+// Swizzle of the D = 64 backward passes' staged tiles (Q/dO in the dK/dV pass, K/V in
+// the dQ pass): 16-byte chunk c of row r is stored at
+// chunk c ^ (r bit 1 -> bit 2, r bits 2-3 -> bits 0-1).  A row-fragment read serves 16
+// lanes (rows r0..r0+15 at one logical chunk) per clock; row bit 0 picks the half of the
+// 256-byte bank window and bits 1-3 the chunk, so the 16 pieces land on 16 distinct
+// 16-byte bank groups (conflict-free: 224 B/clk/CU measured on MI355X against 122 for
+// the swizzle of the other tiles, which leaves row bit 3 out).  The transposed reads run
+// at the same rate with either (165 B/clk/CU).  Row bit 3 changes the swizzle, so the
+// two 8-row halves of a transposed read have separate lane addresses.
+__device__ __forceinline__ int swz_stage64(int row, int chunk) {
+  return chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+}
+
+template <int D>
+__global__ void fa_bwd_dq_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                      const bf16 *__restrict__ V, const bf16 *__restrict__ O,
+                                      const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+                                      float *__restrict__ Delta, bf16 *__restrict__ dQ, int B,
+                                      int Hq, int Hkv, int T, float scale_log2, float scale,
+                                      int paired);
+template <>
+__global__ void fa_bwd_dq_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                          const bf16 *__restrict__ V, const bf16 *__restrict__ O,
+                                          const bf16 *__restrict__ dO,
+                                          const float *__restrict__ LSE, float *__restrict__ Delta,
+                                          bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
+                                          float scale_log2, float scale, int paired);
 template <int D>
 __global__ void fa_bwd_dkdv_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
                                         const bf16 *__restrict__ V, const bf16 *__restrict__ dO,
@@ -43,8 +76,9 @@ __global__ void fa_bwd_dkdv_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf
                                             bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
                                             float scale_log2, float scale, int paired);
 // LDS bytes of the D = 64 dK/dV pass: two 128-row stages of Q and dO tiles plus their
-// -LSE/scale and -Delta rows.
+// -LSE/scale and -Delta rows; of the D = 64 dQ pass: two 128-key stages of K and V tiles.
 constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
+constexpr int kDq64LdsBytes = 2 * 2 * 128 * 64 * 2;
 
 // Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,
 // including launches under stream capture, make no attribute call.

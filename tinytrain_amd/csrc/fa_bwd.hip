@@ -582,7 +582,7 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
                             const void *dout, const float *lse, float *delta, void *dq, int B,
                             int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   const int n_tiles = (T + DqTile<D>::BM - 1) / DqTile<D>::BM;
-  constexpr size_t lds = DqTile<D>::LDS_BYTES;
+  constexpr size_t lds = D == 64 ? kDq64LdsBytes : DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds<fa_bwd_dq_bf16_kernel<D>>(lds);

@@ -17,23 +17,6 @@ namespace ttfa {
 
 namespace {
 
-// LDS byte address of a pointer into the workgroup's shared memory.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const TTFA_LDS void *)p;
-}
-
-// Swizzle of the D = 64 dK/dV pass's Q/dO tiles: 16-byte chunk c of row r is stored at
-// chunk c ^ (r bit 1 -> bit 2, r bits 2-3 -> bits 0-1).  A row-fragment read serves 16
-// lanes (rows r0..r0+15 at one logical chunk) per clock; row bit 0 picks the half of the
-// 256-byte bank window and bits 1-3 the chunk, so the 16 pieces land on 16 distinct
-// 16-byte bank groups (conflict-free: 224 B/clk/CU measured on MI355X against 122 for
-// the swizzle of the other tiles, which leaves row bit 3 out).  The transposed reads run
-// at the same rate with either (165 B/clk/CU).  Row bit 3 changes the swizzle, so the
-// two 8-row halves of a transposed read have separate lane addresses.
-__device__ __forceinline__ int swz_dkv64(int row, int chunk) {
-  return chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
-}
-
 // One 128-row stage of the D = 64 dK/dV pass for one wave, as a hand-scheduled
 // instruction stream (dkdv64_item.inc, written by gen_dkdv64_asm.py): for each of the
 // stage's 32-row query blocks, S - LSE/scale = Q K^T - LSE/scale and dP - Delta =
@@ -106,7 +89,7 @@ __device__ __forceinline__ void dkdv_rows64(bf16 *lds, const DkvHead &hd, int kt
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int e = 256 * i + tid, row = e / CH, pc = e % CH;
-    voff[i] = (uint32_t)(row * D + swz_dkv64(row, pc) * 8) * 2;
+    voff[i] = (uint32_t)(row * D + swz_stage64(row, pc) * 8) * 2;
   }
   auto load_item = [&](int stage) {
     char *st = reinterpret_cast<char *>(lds) + stage * STAGE_BYTES;
@@ -155,13 +138,13 @@ __device__ __forceinline__ void dkdv_rows64(bf16 *lds, const DkvHead &hd, int kt
   const uint32_t base = lds_addr(lds);
   const int g16 = lane >> 4, r4 = (lane >> 2) & 3, c4 = lane & 3;
 #pragma unroll
-  for (int kk = 0; kk < 4; ++kk) aR[kk] = base + lq * 128 + swz_dkv64(lq, 2 * kk + lg) * 16;
+  for (int kk = 0; kk < 4; ++kk) aR[kk] = base + lq * 128 + swz_stage64(lq, 2 * kk + lg) * 16;
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int row = 4 * (g16 >> 1) + r4 + 8 * h, col = 32 * db + 16 * (g16 & 1) + 4 * c4;
-      aT[db][h] = base + row * 128 + (swz_dkv64(row, col >> 3) * 8 + (col & 7)) * 2;
+      aT[db][h] = base + row * 128 + (swz_stage64(row, col >> 3) * 8 + (col & 7)) * 2;
     }
   const uint32_t aN = base + 2 * TILE_BYTES + 16 * lg;
   const int dl = lq - 4 * lg;
