@@ -28,19 +28,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const TTFA_LDS void *)p;
 }
 
-// Swizzle of the D = 64 backward passes' staged tiles (Q/dO in the dK/dV pass, K/V in
-// the dQ pass): 16-byte chunk c of row r is stored at
-// chunk c ^ (r bit 1 -> bit 2, r bits 2-3 -> bits 0-1).  A row-fragment read serves 16
-// lanes (rows r0..r0+15 at one logical chunk) per clock; row bit 0 picks the half of the
-// 256-byte bank window and bits 1-3 the chunk, so the 16 pieces land on 16 distinct
-// 16-byte bank groups (conflict-free: 224 B/clk/CU measured on MI355X against 122 for
-// the swizzle of the other tiles, which leaves row bit 3 out).  The transposed reads run
-// at the same rate with either (165 B/clk/CU).  Row bit 3 changes the swizzle, so the
-// two 8-row halves of a transposed read have separate lane addresses.
-__device__ __forceinline__ int swz_stage64(int row, int chunk) {
-  return chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
-}
-
 template <int D>
 __global__ void fa_bwd_dq_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
                                       const bf16 *__restrict__ V, const bf16 *__restrict__ O,
