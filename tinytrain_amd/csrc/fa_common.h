@@ -112,14 +112,29 @@ __device__ __forceinline__ int swz_stage64(int row, int chunk) {
   return chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
 }
 
-template <int D>
-__device__ __forceinline__ int lds_off(int row, int col) {  // element offset of (row, col)
-  return row * D + (swz<D>(row, col >> 3) << 3) + (col & 7);
+// The D = 128 counterpart (256-byte rows): row bits 0-1 -> chunk bits 2-3, row bits 2-3 ->
+// bits 0-1, so a row-fragment read's 16 rows land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz_rows128(int row, int chunk) {
+  return chunk ^ (((row & 3) << 2) | ((row >> 2) & 3));
 }
 
-template <int D>
+// Tile layout L: 0 = swz<D>, 1 = the swizzle of D with conflict-free row reads
+// (swz_stage64 / swz_rows128).  Loads and reads of one tile use the same L.
+template <int D, int L>
+__device__ __forceinline__ int swz_l(int row, int chunk) {
+  if constexpr (L == 0) return swz<D>(row, chunk);
+  else if constexpr (D == 64) return swz_stage64(row, chunk);
+  else return swz_rows128(row, chunk);
+}
+
+template <int D, int L = 0>
+__device__ __forceinline__ int lds_off(int row, int col) {  // element offset of (row, col)
+  return row * D + (swz_l<D, L>(row, col >> 3) << 3) + (col & 7);
+}
+
+template <int D, int L = 0>
 __device__ __forceinline__ bf16x8 lds_read_row8(const bf16 *tile, int row, int chunk) {
-  return *reinterpret_cast<const bf16x8 *>(tile + row * D + (swz<D>(row, chunk) << 3));
+  return *reinterpret_cast<const bf16x8 *>(tile + row * D + (swz_l<D, L>(row, chunk) << 3));
 }
 
 // The pointer is __restrict__ so that, once inlined, the read carries alias-scope
@@ -136,13 +151,13 @@ __device__ __forceinline__ bf16x4 lds_read_tr(const bf16 *__restrict__ p) {
 // read transposed from a row-major [row][col] LDS tile.  Slot s of lane l holds
 // tile[R0 + 8*(s/4) + 4*(l/32) + s%4][C0 + l%32], i.e. the row set a lane owns in a
 // 32x32 MFMA result, which is what lets a result tile feed the next MFMA as-is.
-template <int D>
+template <int D, int L = 0>
 __device__ __forceinline__ bf16x8 lds_read_trT(const bf16 *tile, int R0, int C0, int lane) {
   const int g16 = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
   const int row = R0 + 4 * (g16 >> 1) + r;
   const int col = C0 + 16 * (g16 & 1) + 4 * c;
-  bf16x4 lo = lds_read_tr(tile + lds_off<D>(row, col));
-  bf16x4 hi = lds_read_tr(tile + lds_off<D>(row + 8, col));
+  bf16x4 lo = lds_read_tr(tile + lds_off<D, L>(row, col));
+  bf16x4 hi = lds_read_tr(tile + lds_off<D, L>(row + 8, col));
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 

@@ -37,31 +37,8 @@ namespace {
 
 constexpr float kRescaleSlack = 8.0f;
 
-// K/V tile layout of the forward: D = 64 uses swz_stage64 (conflict-free K row reads),
-// D = 128 swz<128>.
-template <int D>
-__device__ __forceinline__ int fwd_swz(int row, int chunk) {
-  if constexpr (D == 64) return swz_stage64(row, chunk);
-  else return swz<D>(row, chunk);
-}
-
-template <int D>
-__device__ __forceinline__ bf16x8 fwd_read_row8(const bf16 *tile, int row, int chunk) {
-  return *reinterpret_cast<const bf16x8 *>(tile + row * D + (fwd_swz<D>(row, chunk) << 3));
-}
-
-// lds_read_trT for the forward's layout: slot s of lane l holds
-// tile[R0 + 8*(s/4) + 4*(l/32) + s%4][C0 + l%32].
-template <int D>
-__device__ __forceinline__ bf16x8 fwd_read_trT(const bf16 *tile, int R0, int C0, int lane) {
-  const int g16 = lane >> 4, r = (lane >> 2) & 3, c = lane & 3;
-  const int row = R0 + 4 * (g16 >> 1) + r;
-  const int col = C0 + 16 * (g16 & 1) + 4 * c;
-  auto off = [&](int rw) { return rw * D + (fwd_swz<D>(rw, col >> 3) << 3) + (col & 7); };
-  bf16x4 lo = lds_read_tr(tile + off(row));
-  bf16x4 hi = lds_read_tr(tile + off(row + 8));
-  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
+// K/V tiles use layout 1 (conflict-free K row reads).
+constexpr int kFwdLayout = 1;
 
 template <int D>
 struct FwdTile {
@@ -85,7 +62,7 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int kk = 0; kk < P::KK; ++kk) kf[kb][kk] = fwd_read_row8<D>(Kt, kb * 32 + lq, 2 * kk + lg);
+    for (int kk = 0; kk < P::KK; ++kk) kf[kb][kk] = lds_read_row8<D, kFwdLayout>(Kt, kb * 32 + lq, 2 * kk + lg);
   f32x16 s[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
@@ -159,7 +136,7 @@ __device__ __forceinline__ void fwd_tile(const bf16 *Kt, const bf16 *Vt, const b
   for (int m = 0; m < 4; ++m) {
     bf16x8 vf[P::DB];
 #pragma unroll
-    for (int db = 0; db < P::DB; ++db) vf[db] = fwd_read_trT<D>(Vt, 16 * m, 32 * db, lane);
+    for (int db = 0; db < P::DB; ++db) vf[db] = lds_read_trT<D, kFwdLayout>(Vt, 16 * m, 32 * db, lane);
 #pragma unroll
     for (int db = 0; db < P::DB; ++db) oacc[db] = mfma32(vf[db], pb[m], oacc[db]);
   }
@@ -203,7 +180,7 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int e = 256 * i + 64 * wave + lane, row = e / CH, pc = e % CH;
-    voff[i] = (uint32_t)(row * D + fwd_swz<D>(row, pc) * 8) * 2;
+    voff[i] = (uint32_t)(row * D + swz_l<D, kFwdLayout>(row, pc) * 8) * 2;
   }
   auto load_tile = [&](int j, int stage) {
     // descriptors re-based at the tile (scalar work): rows past T still read as zero
