@@ -45,9 +45,11 @@ namespace ttfa {
 
 namespace {
 
-// K/V tiles of the dQ pass use layout 1 (conflict-free K/V row reads); the Q/dO tiles of
-// the dK/dV pass keep swz<D> (layout 1 measured 3% slower there at D=128).
+// The K/V tiles of the dQ pass and the Q/dO tiles of the D=128 dK/dV pass use layout 1
+// (conflict-free row reads); the D=64 varlen dK/dV pass keeps swz<64>.
 constexpr int kDqLayout = 1;
+template <int D>
+constexpr int kDkvLayout = D == 128 ? 1 : 0;
 
 template <int D>
 struct DqTile {
@@ -180,8 +182,8 @@ __device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, con
     bf16x8 qa[P::KK], da[P::KK];
 #pragma unroll
     for (int kk = 0; kk < P::KK; ++kk) {
-      qa[kk] = lds_read_row8<D>(Qt, qb * 32 + lq, 2 * kk + lg);
-      da[kk] = lds_read_row8<D>(dOt, qb * 32 + lq, 2 * kk + lg);
+      qa[kk] = lds_read_row8<D, kDkvLayout<D>>(Qt, qb * 32 + lq, 2 * kk + lg);
+      da[kk] = lds_read_row8<D, kDkvLayout<D>>(dOt, qb * 32 + lq, 2 * kk + lg);
     }
     if constexpr (D == 128) {
       s[nb] = ns;
@@ -225,8 +227,8 @@ __device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, con
       bf16x8 dot[P::DB], qt[P::DB];
 #pragma unroll
       for (int db = 0; db < P::DB; ++db) {
-        dot[db] = lds_read_trT<D>(dOt, qb * 32 + 16 * m, 32 * db, lane);
-        qt[db] = lds_read_trT<D>(Qt, qb * 32 + 16 * m, 32 * db, lane);
+        dot[db] = lds_read_trT<D, kDkvLayout<D>>(dOt, qb * 32 + 16 * m, 32 * db, lane);
+        qt[db] = lds_read_trT<D, kDkvLayout<D>>(Qt, qb * 32 + 16 * m, 32 * db, lane);
       }
 #pragma unroll
       for (int db = 0; db < P::DB; ++db) {
@@ -472,7 +474,7 @@ __device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, 
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
       const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
-      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz<D>(row, pc) * 8) * 2;
+      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz_l<D, kDkvLayout<D>>(row, pc) * 8) * 2;
       buf_load16_lds(rq, off, Qt + e0 * 8);
       buf_load16_lds(rdo, off, dOt + e0 * 8);
     }

@@ -80,8 +80,8 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // (8 rows down) has the same XOR and its address is the first one plus an immediate;
 // a swizzle that also separates 16 consecutive rows needs row bit 3 (swz_stage64 and
 // swz_rows128 below: layout 1 of the read helpers, used by the forward's K/V tiles, the
-// dQ pass's K/V tiles and the D = 64 batched dK/dV pass).  swz<D> (layout 0) serves the
-// Q/dO tiles of the D = 128 and varlen dK/dV passes, decode and the O staging of
+// dQ pass's K/V tiles and the batched dK/dV passes' Q/dO tiles).  swz<D> (layout 0)
+// serves the Q/dO tiles of the D = 64 varlen dK/dV pass, decode and the O staging of
 // store_rows.
 //  D = 64 (128-byte rows, row bit 0 picks the half of a 256-byte window): row bit 1 ->
 //    chunk bit 2, row bit 0 -> bit 1, row bit 2 -> bit 0; rows 4k and 4k+2 (4k+1, 4k+3)
