@@ -1,5 +1,6 @@
-"""The generated D = 64 stage schedules of the backward passes (tinytrain_amd/csrc/
-dkdv64_item.inc for the dK/dV pass, dq64_stage.inc for the dQ pass).
+"""The generated stage schedules of the backward passes (tinytrain_amd/csrc/
+dkdv64_item.inc and dkdv128_item.inc for the dK/dV pass at D = 64 and 128, dq64_stage.inc
+for the D = 64 dQ pass).
 
 The generator inserts the LDS waits and hazard padding that the compiler does not add
 inside an asm statement.  This test re-checks the emitted text with an independent
@@ -11,7 +12,12 @@ the CPU instead of computing wrong products on the GPU:
   * no more than 15 LDS reads are outstanding (the lgkmcnt field);
   * an MFMA result is read or overwritten by VALU / LDS only 12 wait states later, a VALU
     result is read by an MFMA only 2 later, a v_exp result by VALU only 1 later;
-  * each variant issues the products, reads and exponentials its blocks need.
+  * each variant issues the products, reads and exponentials its blocks need;
+  * (D = 128 dK/dV) a symbolic replay of the emitted stream: every register carries a tag
+    naming what it holds (a Q/dO row fragment, a transposed fragment, an S or dP partial
+    sum after k-step kk, P, dS, packed P/dS), and each product and softmax step checks
+    the tags of what it reads, so an LDS read placed after its consumer, or a product
+    reading the wrong block's fragments, fails here.
 """
 
 import re
@@ -185,3 +191,163 @@ def test_dq_stream_rules_and_counts(name):
     masked = {"FULL": 0, "RAGGED": 4}.get(name, 1)
     assert count("v_cmp_gt_i32") == 16 * masked
     assert count("v_cvt_pk_bf16_f32") == 8 * n_blocks
+
+
+# ---- D = 128 dK/dV stage (dkdv128_item.inc) -------------------------------------------
+# Register map and operands as the generator's header states them: v[0:15] S of register
+# set 0, v[16:31] its dP, v[32:63] set 1; v[64+4kk] Q row fragments, v[96+4kk] dO ones,
+# v[128+4db] dO^T, v[144+4db] Q^T; %0..%3 dK^T accumulators, %4..%7 dV^T ones, %8..%15 K
+# fragments, %16..%23 V fragments, %24..%27 row-read addresses (k-steps 2p, 2p+1 at +32),
+# %28..%31 transposed-read addresses, %32 the -LSE/scale rows (-Delta at +512).  LDS
+# stage: Q rows at 0, dO rows at +32768, 256 bytes a row, 32-row blocks of 8192 bytes.
+D128_KK, D128_DB = 8, 4
+D128_VARIANTS = {"FULL": [0, 1, 2, 3], "DIAG0": [0, 1, 2, 3], "DIAG1": [1, 2, 3],
+                 "DIAG2": [2, 3], "DIAG3": [3]}
+
+
+def _vrange(tok):
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", tok)
+    if m:
+        return list(range(int(m.group(1)), int(m.group(2)) + 1))
+    return [int(re.fullmatch(r"v(\d+)", tok).group(1))]
+
+
+def _set_of(v):
+    """(register set, 'S' or 'P', index within the 16) of an S/dP register."""
+    rs, r = divmod(v, 32)
+    return rs, ("S" if r < 16 else "P"), r % 16
+
+
+def _dataflow_d128(lines, blocks):
+    """Replays one emitted variant on tags; returns a list of errors."""
+    reg, acc, errs = {}, {}, []
+    for ln in lines:
+        if ln.startswith(("s_nop", "s_waitcnt")):
+            continue
+        m = re.match(r"ds_read_b128 (\S+), %(\d+) offset:(\d+)", ln)
+        if m:
+            dst, addr, off = _vrange(m.group(1)), int(m.group(2)), int(m.group(3))
+            if addr == 32:
+                which, r = divmod(off, 512)
+                tag = ("init", which, r // 128)
+            else:
+                p = addr - 24
+                tensor, r = divmod(off, 32768)
+                lb, r = divmod(r, 8192)
+                tag = ("row", tensor, lb, 2 * p + r // 32)
+            for i, v in enumerate(dst):
+                reg[v] = tag + (i,)
+            continue
+        m = re.match(r"ds_read_b64_tr_b16 (\S+), %(\d+) offset:(\d+)", ln)
+        if m:
+            dst, db, off = _vrange(m.group(1)), int(m.group(2)) - 28, int(m.group(3))
+            tensor, r = divmod(off, 32768)
+            row = r // 256
+            for i, v in enumerate(dst):
+                reg[v] = ("tr", tensor, row // 32, (row % 32) // 16, db, (row % 16) // 8)
+            continue
+        m = re.match(r"v_mfma_f32_32x32x16_bf16 (\S+), (\S+), (\S+), (\S+)", ln)
+        if m:
+            d, a, b, c = m.groups()
+            if d.startswith("%"):  # dK^T / dV^T += (Q^T | dO^T) x (packed dS | P)
+                n = int(d[1:])
+                kind, db = ("dk", n) if n < 4 else ("dv", n - 4)
+                A = [reg.get(v) for v in _vrange(a)]
+                B = [reg.get(v) for v in _vrange(b)]
+                tensor = 0 if kind == "dk" else 1
+                if None in A or any(x[0] != "tr" or x[1] != tensor or x[4] != db for x in A) \
+                        or [x[5] for x in A] != [0, 0, 1, 1] or len({x[2:4] for x in A}) != 1:
+                    errs.append(f"{ln}: A operand {A}")
+                    continue
+                lb, mg = A[0][2], A[0][3]
+                want = "dSk" if kind == "dk" else "Pk"
+                if any(x != (want, lb, mg) for x in B):
+                    errs.append(f"{ln}: B operand {B}, want {(want, lb, mg)}")
+                acc.setdefault((kind, db), []).append((lb, mg))
+                continue
+            D_, A = _vrange(d), [reg.get(v) for v in _vrange(a)]
+            if None in A or any(x[0] != "row" or x[1:4] != A[0][1:4] for x in A):
+                errs.append(f"{ln}: A operand {A}")
+                continue
+            _, tensor, lb, kk = A[0][:4]
+            if int(b[1:]) != (8 if tensor == 0 else 16) + kk:
+                errs.append(f"{ln}: B operand {b} for k-step {kk}")
+            name = "S" if tensor == 0 else "P"
+            if {_set_of(v)[1] for v in D_} != {name}:
+                errs.append(f"{ln}: destination not a {name} block")
+            want = ("init", tensor, lb) if kk == 0 else (name, lb, kk - 1)
+            for v in D_:
+                x = reg.get(v)
+                if x is None or x[:3] != want:
+                    errs.append(f"{ln}: C register v{v} holds {x}, want {want}")
+                    break
+            for v in D_:
+                reg[v] = (name, lb, kk)
+            continue
+        m = re.match(r"v_exp_f32 v(\d+), v(\d+)", ln)
+        if m:
+            v = int(m.group(1))
+            x = reg.get(v)
+            if x is None or x[0] != "S" or x[2] != D128_KK - 1:
+                errs.append(f"{ln}: exponential of {x}")
+            reg[v] = ("p", x[1] if x else None)
+            continue
+        m = re.match(r"v_mul_f32 v(\d+), v(\d+), v(\d+)", ln)
+        if m:  # dS = P * (dP - Delta)
+            d, s_, p_ = (int(g) for g in m.groups())
+            x, y = reg.get(s_), reg.get(p_)
+            if not (x and y and x[0] == "p" and y[0] == "P" and y[2] == D128_KK - 1 and x[1] == y[1]):
+                errs.append(f"{ln}: dS from {x} and {y}")
+            reg[d] = ("dS", x[1] if x else None)
+            continue
+        m = re.match(r"v_cvt_pk_bf16_f32 v(\d+), v(\d+), v(\d+)", ln)
+        if m:
+            d, s0, s1 = (int(g) for g in m.groups())
+            rs, name, r = _set_of(d)
+            want = "p" if name == "S" else "dS"
+            x0, x1 = reg.get(s0), reg.get(s1)
+            if not (x0 and x1 and x0[0] == want and x1 == x0):
+                errs.append(f"{ln}: packs {x0} and {x1}")
+            reg[d] = ("Pk" if name == "S" else "dSk", x0[1] if x0 else None, r // 8)
+            continue
+    for kind in ("dk", "dv"):
+        for db in range(D128_DB):
+            want = [(lb, mg) for lb in blocks for mg in range(2)]
+            if acc.get((kind, db), []) != want:
+                errs.append(f"{kind} column block {db}: contributions {acc.get((kind, db))}, want {want}")
+    return errs
+
+
+def test_d128_committed_file_is_the_generator_output():
+    gen = _gen("gen_dkdv128_asm")
+    assert (CSRC / "dkdv128_item.inc").read_text() == gen.render(), \
+        "dkdv128_item.inc is stale: run python tinytrain_amd/csrc/gen_dkdv128_asm.py"
+
+
+@pytest.mark.parametrize("name", list(D128_VARIANTS))
+def test_d128_stream_rules_counts_and_dataflow(name):
+    var = _variants(_gen("gen_dkdv128_asm").render(), "TTFA_DKDV128_STAGE_ASM", "dk128")
+    assert set(var) == set(D128_VARIANTS)
+    lines = var[name]
+    _check_stream(lines)
+    n_blocks = len(D128_VARIANTS[name])
+    count = lambda p: sum(1 for ln in lines if ln.startswith(p))
+    assert count("v_mfma") == 32 * n_blocks           # S, dP: 16; dV, dK: 16 per block
+    assert count("ds_read_b128") == 24 * n_blocks     # 8 init, 16 row fragments
+    assert count("ds_read_b64_tr_b16") == 32 * n_blocks
+    assert count("v_exp_f32") == 16 * n_blocks
+    assert count("v_cmp_lt_i32") == (0 if name == "FULL" else 16)
+    assert count("v_cvt_pk_bf16_f32") == 16 * n_blocks
+    assert _dataflow_d128(lines, D128_VARIANTS[name]) == []
+
+
+def test_d128_dataflow_check_catches_a_misplaced_read():
+    """Moving the first -LSE/scale read of the second block to just after that block's
+    first S product (the product then starts from stale registers) fails the replay."""
+    lines = _variants(_gen("gen_dkdv128_asm").render(), "TTFA_DKDV128_STAGE_ASM", "dk128")["FULL"]
+    inits = [k for k, ln in enumerate(lines) if re.match(r"ds_read_b128 \S+, %32 offset:(128|160|192|224)$", ln)]
+    i = inits[0]
+    j = next(k for k, ln in enumerate(lines) if k > i and ln.startswith("v_mfma") and ", %8, " in ln)
+    moved = lines[:i] + lines[i + 1:j] + [lines[j], lines[i]] + lines[j + 1:]
+    assert _dataflow_d128(lines, D128_VARIANTS["FULL"]) == []
+    assert _dataflow_d128(moved, D128_VARIANTS["FULL"]) != []

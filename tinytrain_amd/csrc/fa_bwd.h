@@ -62,9 +62,17 @@ __global__ void fa_bwd_dkdv_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf
                                             const float *__restrict__ Delta, bf16 *__restrict__ dK,
                                             bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
                                             float scale_log2, float scale, int paired);
-// LDS bytes of the D = 64 dK/dV pass: two 128-row stages of Q and dO tiles plus their
+template <>
+__global__ void fa_bwd_dkdv_bf16_kernel<128>(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                             const bf16 *__restrict__ V, const bf16 *__restrict__ dO,
+                                             const float *__restrict__ LSE,
+                                             const float *__restrict__ Delta, bf16 *__restrict__ dK,
+                                             bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
+                                             float scale_log2, float scale, int paired);
+// LDS bytes of the batched dK/dV passes: two 128-row stages of Q and dO tiles plus their
 // -LSE/scale and -Delta rows; of the D = 64 dQ pass: two 128-key stages of K and V tiles.
 constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
+constexpr int kDkv128LdsBytes = 2 * (2 * 128 * 128 * 2 + 2 * 128 * 4);
 constexpr int kDq64LdsBytes = 2 * 2 * 128 * 64 * 2;
 
 // Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,

@@ -608,7 +608,7 @@ static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const
                               const float *lse, const float *delta, void *dk, void *dv, int B,
                               int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   const int n_ktiles = (T + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
-  constexpr size_t lds = D == 64 ? kDkv64LdsBytes : DkvTile<D>::LDS_BYTES;
+  constexpr size_t lds = D == 64 ? kDkv64LdsBytes : kDkv128LdsBytes;
   auto kern = fa_bwd_dkdv_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds<fa_bwd_dkdv_bf16_kernel<D>>(lds);

@@ -317,6 +317,9 @@ def hoist_lds(ops, lead=LDS_LEAD):
             if dst & (set(c.reads) | set(c.writes)):
                 cons = i
                 break
+        if legal > cons:
+            raise SystemExit(f'LDS read {op.text} cannot go before its consumer {core[cons].text}: '
+                             'the registers it fills are still in use there')
         want, need = cons, lead
         while need > 0 and want > legal:
             want -= 1
