@@ -197,9 +197,10 @@ def test_dq_stream_rules_and_counts(name):
 # Register map and operands as the generator's header states them: v[0:15] S of register
 # set 0, v[16:31] its dP, v[32:63] set 1; v[64+4kk] Q row fragments, v[96+4kk] dO ones,
 # v[128+4db] dO^T, v[144+4db] Q^T; %0..%3 dK^T accumulators, %4..%7 dV^T ones, %8..%15 K
-# fragments, %16..%23 V fragments, %24..%27 row-read addresses (k-steps 2p, 2p+1 at +32),
-# %28..%31 transposed-read addresses, %32 the -LSE/scale rows (-Delta at +512).  LDS
-# stage: Q rows at 0, dO rows at +32768, 256 bytes a row, 32-row blocks of 8192 bytes.
+# fragments, %16..%23 V fragments, %24+kk row-read addresses of k-step kk, %32+2db+h
+# transposed-read addresses (column block db, 8-row half h), %40 the -LSE/scale rows
+# (-Delta at +512).  LDS stage: Q rows at 0, dO rows at +32768, 256 bytes a row, 32-row
+# blocks of 8192 bytes.
 D128_KK, D128_DB = 8, 4
 D128_VARIANTS = {"FULL": [0, 1, 2, 3], "DIAG0": [0, 1, 2, 3], "DIAG1": [1, 2, 3],
                  "DIAG2": [2, 3], "DIAG3": [3]}
@@ -227,24 +228,27 @@ def _dataflow_d128(lines, blocks):
         m = re.match(r"ds_read_b128 (\S+), %(\d+) offset:(\d+)", ln)
         if m:
             dst, addr, off = _vrange(m.group(1)), int(m.group(2)), int(m.group(3))
-            if addr == 32:
+            if addr == 40:
                 which, r = divmod(off, 512)
                 tag = ("init", which, r // 128)
             else:
-                p = addr - 24
                 tensor, r = divmod(off, 32768)
-                lb, r = divmod(r, 8192)
-                tag = ("row", tensor, lb, 2 * p + r // 32)
+                if r % 8192:
+                    errs.append(f"{ln}: offset inside a block")
+                tag = ("row", tensor, r // 8192, addr - 24)
             for i, v in enumerate(dst):
                 reg[v] = tag + (i,)
             continue
         m = re.match(r"ds_read_b64_tr_b16 (\S+), %(\d+) offset:(\d+)", ln)
         if m:
-            dst, db, off = _vrange(m.group(1)), int(m.group(2)) - 28, int(m.group(3))
+            dst, off = _vrange(m.group(1)), int(m.group(3))
+            db, h = divmod(int(m.group(2)) - 32, 2)
             tensor, r = divmod(off, 32768)
             row = r // 256
+            if row % 16:
+                errs.append(f"{ln}: offset inside a 16-row group")
             for i, v in enumerate(dst):
-                reg[v] = ("tr", tensor, row // 32, (row % 32) // 16, db, (row % 16) // 8)
+                reg[v] = ("tr", tensor, row // 32, (row % 32) // 16, db, h)
             continue
         m = re.match(r"v_mfma_f32_32x32x16_bf16 (\S+), (\S+), (\S+), (\S+)", ln)
         if m:
@@ -345,7 +349,7 @@ def test_d128_dataflow_check_catches_a_misplaced_read():
     """Moving the first -LSE/scale read of the second block to just after that block's
     first S product (the product then starts from stale registers) fails the replay."""
     lines = _variants(_gen("gen_dkdv128_asm").render(), "TTFA_DKDV128_STAGE_ASM", "dk128")["FULL"]
-    inits = [k for k, ln in enumerate(lines) if re.match(r"ds_read_b128 \S+, %32 offset:(128|160|192|224)$", ln)]
+    inits = [k for k, ln in enumerate(lines) if re.match(r"ds_read_b128 \S+, %40 offset:(128|160|192|224)$", ln)]
     i = inits[0]
     j = next(k for k, ln in enumerate(lines) if k > i and ln.startswith("v_mfma") and ", %8, " in ln)
     moved = lines[:i] + lines[i + 1:j] + [lines[j], lines[i]] + lines[j + 1:]

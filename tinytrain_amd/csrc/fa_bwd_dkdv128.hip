@@ -24,20 +24,22 @@ namespace {
 // and dK^T += Q^T dS over the 4 column blocks, with the blocks software-pipelined against
 // each other.  mode (wave-uniform) 0: all four blocks lie below the wave's keys; 1 + w:
 // the stage holding the diagonal for wave w.  The accumulators and the K/V fragments stay
-// in AGPRs; aR are the lane's LDS byte addresses of the row-fragment reads for k-steps 2p
-// (2p+1 at +32), aT those of the transposed reads per column block (the lower 8 rows at
-// +2048), aN that of the -LSE/scale rows; dl = lq - 4lg places the diagonal mask.
+// in AGPRs; aR are the lane's LDS byte addresses of the row-fragment reads per k-step, aT
+// those of the transposed reads per column block and 8-row half (2db + h), aN that of the
+// -LSE/scale rows; dl = lq - 4lg places the diagonal mask.
 #define TTFA_DKDV128_OPERANDS                                                                \
   : "+a"(dk[0]), "+a"(dk[1]), "+a"(dk[2]), "+a"(dk[3]), "+a"(dv[0]), "+a"(dv[1]),            \
     "+a"(dv[2]), "+a"(dv[3])                                                                 \
   : "a"(kf[0]), "a"(kf[1]), "a"(kf[2]), "a"(kf[3]), "a"(kf[4]), "a"(kf[5]), "a"(kf[6]),     \
     "a"(kf[7]), "a"(vf[0]), "a"(vf[1]), "a"(vf[2]), "a"(vf[3]), "a"(vf[4]), "a"(vf[5]),     \
-    "a"(vf[6]), "a"(vf[7]), "v"(aR[0]), "v"(aR[1]), "v"(aR[2]), "v"(aR[3]), "v"(aT[0]),     \
-    "v"(aT[1]), "v"(aT[2]), "v"(aT[3]), "v"(aN), "s"(scale_log2), "v"(dl), "s"(mode)        \
+    "a"(vf[6]), "a"(vf[7]), "v"(aR[0]), "v"(aR[1]), "v"(aR[2]), "v"(aR[3]), "v"(aR[4]),     \
+    "v"(aR[5]), "v"(aR[6]), "v"(aR[7]), "v"(aT[0]), "v"(aT[1]), "v"(aT[2]), "v"(aT[3]),     \
+    "v"(aT[4]), "v"(aT[5]), "v"(aT[6]), "v"(aT[7]), "v"(aN), "s"(scale_log2), "v"(dl),      \
+    "s"(mode)                                                                                \
   : TTFA_DKDV128_ITEM_CLOBBERS, "memory"
 __device__ __forceinline__ void dkdv128_stage(f32x16 (&dk)[4], f32x16 (&dv)[4], const bf16x8 (&kf)[8],
-                                              const bf16x8 (&vf)[8], const uint32_t (&aR)[4],
-                                              const uint32_t (&aT)[4], uint32_t aN,
+                                              const bf16x8 (&vf)[8], const uint32_t (&aR)[8],
+                                              const uint32_t (&aT)[8], uint32_t aN,
                                               float scale_log2, int dl, int mode) {
   asm volatile(TTFA_DKDV128_STAGE_ASM TTFA_DKDV128_OPERANDS);
 }
@@ -90,7 +92,7 @@ __device__ __forceinline__ void dkdv_rows128(bf16 *lds, const DkvHead &hd, int k
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
     const int e = 256 * i + tid, row = e / CH, pc = e % CH;
-    voff[i] = (uint32_t)(row * D + swz<D>(row, pc) * 8) * 2;
+    voff[i] = (uint32_t)(row * D + swz_rows128(row, pc) * 8) * 2;
   }
   auto load_item = [&](int stage) {
     char *st = reinterpret_cast<char *>(lds) + stage * STAGE_BYTES;
@@ -139,19 +141,22 @@ __device__ __forceinline__ void dkdv_rows128(bf16 *lds, const DkvHead &hd, int k
                    "=a"(dvacc[0]), "=a"(dvacc[1]), "=a"(dvacc[2]), "=a"(dvacc[3])
                  : "v"(z));
   }
-  // the lane's LDS addresses in stage 0 (stage 1 adds STAGE_BYTES).  swz<128> XORs the
-  // chunk with row bits 0-2 only and leaves chunk bit 1 alone, so k-step 2p+1's row read
-  // is k-step 2p's plus 32 bytes and a transposed read's lower 8 rows are its upper 8
-  // plus 2048.
-  uint32_t aR[4], aT[4];
+  // the lane's LDS addresses in stage 0, query block 0 (stage 1 adds STAGE_BYTES, block
+  // lb 8192 lb, the dO tile 32768).  swz_rows128 XORs the chunk with row bits 0-3, so the
+  // other query blocks and the 16-row groups of the transposed reads are constant offsets
+  // but each k-step and each 8-row half needs an address of its own.
+  uint32_t aR[8], aT[8];
   const uint32_t base = lds_addr(lds);
   const int g16 = lane >> 4, r4 = (lane >> 2) & 3, c4 = lane & 3;
 #pragma unroll
-  for (int p = 0; p < 4; ++p) aR[p] = base + lq * 256 + swz<D>(lq, 4 * p + lg) * 16;
+  for (int kk = 0; kk < 8; ++kk) aR[kk] = base + lq * 256 + swz_rows128(lq, 2 * kk + lg) * 16;
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
-    const int row = 4 * (g16 >> 1) + r4, col = 32 * db + 16 * (g16 & 1) + 4 * c4;
-    aT[db] = base + row * 256 + (swz<D>(row, col >> 3) * 8 + (col & 7)) * 2;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 4 * (g16 >> 1) + r4 + 8 * h, col = 32 * db + 16 * (g16 & 1) + 4 * c4;
+      aT[2 * db + h] = base + row * 256 + (swz_rows128(row, col >> 3) * 8 + (col & 7)) * 2;
+    }
   }
   const uint32_t aN = base + 2 * TILE_BYTES + 16 * lg;
   const int dl = lq - 4 * lg;
@@ -166,8 +171,12 @@ __device__ __forceinline__ void dkdv_rows128(bf16 *lds, const DkvHead &hd, int k
   for (int it = 0; it < n_items; ++it) {
     if (it + 1 < n_items) load_item((it + 1) & 1);
     const uint32_t so = (it & 1) * STAGE_BYTES;
-    const uint32_t r[4] = {aR[0] + so, aR[1] + so, aR[2] + so, aR[3] + so};
-    const uint32_t t[4] = {aT[0] + so, aT[1] + so, aT[2] + so, aT[3] + so};
+    uint32_t r[8], t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      r[i] = aR[i] + so;
+      t[i] = aT[i] + so;
+    }
     // the stage that holds the diagonal (qt == kt): wave w's keys see its blocks w..3
     const int mode = qt != kt ? 0 : 1 + wave_u;
     dkdv128_stage(dkacc, dvacc, kf, vf, r, t, aN + so, scale_log2, dl, mode);

@@ -19,12 +19,14 @@ Register map (fixed; the statement clobbers v[0:159]):
   v[64:95] Q row fragments (k-step kk at v[64+4kk]), v[96:127] dO row fragments,
   v[128:143] dO^T fragments (column block db at +4db), v[144:159] Q^T fragments.
 Operands: %0..%3 the dK^T accumulators (column blocks db), %4..%7 the dV^T ones,
-%8..%15 the K fragments (k-step kk), %16..%23 the V fragments, all in AGPRs; %24..%27 the
-LDS byte addresses of the row-fragment reads for k-steps 2p (k-step 2p+1 at +32: the
-tiles use swz<128>, whose XOR leaves chunk bit 1 alone), %28..%31 those of the transposed
-reads per column block (the lower 8 rows at +2048: the XOR depends on row bits 0-2 only),
-%32 the -LSE/scale rows' address, %33 the SGPR scale*log2(e), %34 lq - 4lg (the diagonal
-mask), %35 the SGPR mode (0: FULL, 1 + w: DIAG<w>).
+%8..%15 the K fragments (k-step kk), %16..%23 the V fragments, all in AGPRs; %24..%31 the
+LDS byte addresses of the row-fragment reads per k-step, %32..%39 those of the transposed
+reads (column block db, half h at %32+2db+h), %40 the -LSE/scale rows' address, %41 the
+SGPR scale*log2(e), %42 lq - 4lg (the diagonal mask), %43 the SGPR mode (0: FULL,
+1 + w: DIAG<w>).  The tiles use swz_rows128, whose XOR takes row bits 0-3 into all four
+chunk bits (a row read's 16 rows hit 16 distinct bank groups), so every k-step and every
+8-row half has an address of its own; the 32-row blocks (+8192 bytes), the dO tile
+(+32768) and the 16-row groups of the transposed reads (+4096) are constant offsets.
 
 usage: python gen_dkdv128_asm.py [out.inc]
 """
@@ -54,19 +56,19 @@ OP_DK = [0, 1, 2, 3]
 OP_DV = [4, 5, 6, 7]
 OP_KF = list(range(8, 16))
 OP_VF = list(range(16, 24))
-OP_AR = [24, 25, 26, 27]     # row-fragment reads, k-steps 2p and 2p+1
-OP_AT = [28, 29, 30, 31]     # transposed reads, column block db
-OP_AN = 32
-OP_SCALE = 33
-OP_DL = 34
-OP_MODE = 35
+OP_AR = list(range(24, 32))  # row-fragment reads, k-step kk
+OP_AT = list(range(32, 40))  # transposed reads, column block db, half h: 2db + h
+OP_AN = 40
+OP_SCALE = 41
+OP_DL = 42
+OP_MODE = 43
 
 
 def l_rows(lb, kk, tensor):
     """Q (tensor 0) or dO (tensor 1) row fragment of k-step kk, LDS block lb."""
     dst = (QA if tensor == 0 else DA) + 4 * kk
-    off = DO_OFF * tensor + BLOCK_BYTES * lb + 32 * (kk & 1)
-    return Op(f'ds_read_b128 {vt(dst, 4)}, %{OP_AR[kk >> 1]} offset:{off}', 'lds', writes=vr(dst, 4))
+    off = DO_OFF * tensor + BLOCK_BYTES * lb
+    return Op(f'ds_read_b128 {vt(dst, 4)}, %{OP_AR[kk]} offset:{off}', 'lds', writes=vr(dst, 4))
 
 
 def l_init(rb, lb, a, which):
@@ -81,8 +83,8 @@ def l_tr(lb, m, db, tensor, h):
     """Half h of the transposed fragment (query rows 32lb+16m.., columns 32db..) of Q
     (tensor 0, -> Q^T registers) or dO (tensor 1, -> dO^T registers)."""
     dst = (QT if tensor == 0 else DOT) + 4 * db + 2 * h
-    off = DO_OFF * tensor + (32 * lb + 16 * m + 8 * h) * ROW_BYTES
-    return Op(f'ds_read_b64_tr_b16 {vt(dst, 2)}, %{OP_AT[db]} offset:{off}', 'lds', writes=vr(dst, 2))
+    off = DO_OFF * tensor + (32 * lb + 16 * m) * ROW_BYTES
+    return Op(f'ds_read_b64_tr_b16 {vt(dst, 2)}, %{OP_AT[2 * db + h]} offset:{off}', 'lds', writes=vr(dst, 2))
 
 
 def l_tr_set(lb, m, tensor):
