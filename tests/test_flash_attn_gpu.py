@@ -102,6 +102,34 @@ def test_config_parity(name):
             assert_close_abs(nm, got, want, tol, f"[{name} vs eager fp32]")
 
 
+# ------------------------------------------------- the 256-row dQ pass at D = 128
+@pytest.mark.parametrize("B, H, H_kv, T", [
+    (1, 64, 8, 2000),   # T ragged to the 128-key stages and 256-row tiles
+    (2, 32, 4, 2048),
+])
+def test_wide_dq_pass(B, H, H_kv, T):
+    """Shapes whose 256-row pairs fill the 256 resident workgroup slots of an MI355X, so
+    the dQ pass runs its 64-rows-per-wave kernel (the smaller shapes above take the
+    128-row one); two (batch, kv-head) groups checked against the oracle."""
+    D = 128
+    announce(f"wide dQ B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    q, k, v, do = make_custom(B, H, H_kv, T, D, torch.bfloat16, seed=3)
+    o, M, dq, dk, dv = _run(q, k, v, do)
+    G = H // H_kv
+    for b, hk in ((0, 0), (B - 1, H_kv - 1)):
+        hs = slice(hk * G, (hk + 1) * G)
+        sl = lambda t, kv=False: t[b:b + 1, hk:hk + 1] if kv else t[b:b + 1, hs]
+        want = reference_outputs(sl(q), sl(k, True), sl(v, True), sl(do), dtype=torch.float32)
+        got = (sl(o), sl(M), sl(dq), sl(dk, True), sl(dv, True))
+        # make_custom's dO is not scaled down, so dK/dV sums over G*T rows reach values
+        # whose bf16 rounding alone exceeds an absolute bound: relative + absolute, as in
+        # the reference's parity test above
+        assert_close_abs("lse", got[1], want[1], TOL_LSE, f"[b={b},hk={hk}]")
+        for i, nm in ((0, "o"), (2, "dq"), (3, "dk"), (4, "dv")):
+            torch.testing.assert_close(got[i].float(), want[i].float(), rtol=3e-2, atol=3e-2,
+                                       msg=lambda m, n=nm: f"{n} mismatch [b={b},hk={hk}]\n{m}")
+
+
 # ------------------------------------------------- edge shapes
 @pytest.mark.parametrize("B, H, H_kv, T, D, dtype", [
     (1, 1, 1, 1, 64, torch.bfloat16),      # a single row

@@ -355,3 +355,187 @@ def test_d128_dataflow_check_catches_a_misplaced_read():
     moved = lines[:i] + lines[i + 1:j] + [lines[j], lines[i]] + lines[j + 1:]
     assert _dataflow_d128(lines, D128_VARIANTS["FULL"]) == []
     assert _dataflow_d128(moved, D128_VARIANTS["FULL"]) != []
+
+
+# ---- D = 128 dQ stage (dq128_stage.inc) ------------------------------------------------
+# Register map as the generator's header states it: v[0:15] S^T of register set 0,
+# v[16:31] its dP^T, v[32:63] set 1; v[64+4kk] K row fragments, v[96+4kk] V ones,
+# v[128+16m+4db] K^T fragments; v[160+kk] row-read addresses (%0 ^ 32kk), v[168+i]
+# transposed-read addresses (%1 ^ 32i, i = 2db + h).  AGPRs: a[64qg+16db:+15] dQ^T
+# accumulators, a[128+32qg+4kk:+3] Q fragments, a[192+32qg+4kk:+3] dO fragments.
+# Operands: %2 scale, %3+qg -LSE, %5+qg -Delta, %7+qg mask bound.  LDS stage: K rows at
+# 0, V rows at +32768, 256 bytes a row, 32-key blocks of 8192 bytes.
+
+
+def _agpr_base(tok):
+    m = re.fullmatch(r"a\[(\d+):(\d+)\]", tok)
+    return int(m.group(1)) if m else None
+
+
+def _dataflow_dq128(lines):
+    """Replays one emitted variant of the dQ stream on tags; returns a list of errors."""
+    reg, acc, errs = {}, {}, []
+    for ln in lines:
+        if ln.startswith(("s_nop", "s_waitcnt")):
+            continue
+        m = re.match(r"v_(mov|xor)_b32 v(\d+), (?:(\d+), )?(%\d+)$", ln)
+        if m and int(m.group(2)) >= 160:
+            v, k, base = int(m.group(2)), int(m.group(3) or 0), m.group(4)
+            reg[v] = ("addr", base, k)
+            continue
+        m = re.match(r"ds_read_b128 (\S+), v(\d+) offset:(\d+)", ln)
+        if m:
+            dst, a, off = _vrange(m.group(1)), int(m.group(2)), int(m.group(3))
+            kk = a - 160
+            if reg.get(a) != ("addr", "%0", 32 * kk):
+                errs.append(f"{ln}: address register holds {reg.get(a)}")
+            tensor, r = divmod(off, 32768)
+            if r % 8192:
+                errs.append(f"{ln}: offset inside a block")
+            for i, v in enumerate(dst):
+                reg[v] = ("row", tensor, r // 8192, kk)
+            continue
+        m = re.match(r"ds_read_b64_tr_b16 (\S+), v(\d+) offset:(\d+)", ln)
+        if m:
+            dst, a, off = _vrange(m.group(1)), int(m.group(2)), int(m.group(3))
+            i = a - 168
+            if reg.get(a) != ("addr", "%1", 32 * i):
+                errs.append(f"{ln}: address register holds {reg.get(a)}")
+            db, h = divmod(i, 2)
+            row = off // 256
+            if off % 256 or (row % 16) // 8 != h:
+                errs.append(f"{ln}: offset {off} is not half {h} of a 16-row group")
+            for v in dst:
+                reg[v] = ("kt", row // 32, (row % 32) // 16, db, h)
+            continue
+        m = re.match(r"v_mov_b32 v(\d+), %(\d+)$", ln)
+        if m:
+            reg[int(m.group(1))] = ("ndelta", int(m.group(2)) - 5)
+            continue
+        m = re.match(r"v_mfma_f32_32x32x16_bf16 (\S+), (\S+), (\S+), (\S+)", ln)
+        if m:
+            d, a, b, c = m.groups()
+            if d.startswith("a"):  # dQ^T += K^T dS^T
+                qg, db = divmod(_agpr_base(d), 64)
+                db //= 16
+                A = [reg.get(v) for v in _vrange(a)]
+                B = [reg.get(v) for v in _vrange(b)]
+                if None in A or any(x[0] != "kt" or x[3] != db for x in A) \
+                        or [x[4] for x in A] != [0, 0, 1, 1] or len({x[1:3] for x in A}) != 1:
+                    errs.append(f"{ln}: A operand {A}")
+                    continue
+                lb, mg = A[0][1], A[0][2]
+                if any(x != ("dSk", lb, qg, mg) for x in B):
+                    errs.append(f"{ln}: B operand {B}, want {('dSk', lb, qg, mg)}")
+                acc.setdefault((qg, db), []).append((lb, mg))
+                continue
+            D_, A = _vrange(d), [reg.get(v) for v in _vrange(a)]
+            if None in A or any(x[0] != "row" or x[1:] != A[0][1:] for x in A):
+                errs.append(f"{ln}: A operand {A}")
+                continue
+            _, tensor, lb, kk = A[0]
+            bb = _agpr_base(b) - (128 if tensor == 0 else 192)
+            qg, bkk = divmod(bb // 4, 8)
+            if bkk != kk or not 0 <= qg < 2:
+                errs.append(f"{ln}: B operand {b} for k-step {kk}")
+            name = "S" if tensor == 0 else "P"
+            if {_set_of(v)[1] for v in D_} != {name}:
+                errs.append(f"{ln}: destination not a {name} block")
+            if kk == 0 and tensor == 0:
+                if c != "0":
+                    errs.append(f"{ln}: S^T chain does not start at 0")
+            else:
+                want = ("ndelta", qg) if kk == 0 else (name, lb, qg, kk - 1)
+                bad = [v for v in D_ if reg.get(v) != want]
+                if bad:
+                    errs.append(f"{ln}: C register v{bad[0]} holds {reg.get(bad[0])}, want {want}")
+            for v in D_:
+                reg[v] = (name, lb, qg, kk)
+            continue
+        m = re.match(r"v_fma_f32 v(\d+), v(\d+), %2, %(\d+)$", ln)
+        if m:
+            v, qg = int(m.group(1)), int(m.group(3)) - 3
+            x = reg.get(v)
+            if not (x and x[0] == "S" and x[2] == qg and x[3] == 7):
+                errs.append(f"{ln}: scaled {x} with row group {qg}'s LSE")
+            reg[v] = ("x", x[1] if x else None, qg)
+            continue
+        m = re.match(r"v_exp_f32 v(\d+), v(\d+)", ln)
+        if m:
+            v = int(m.group(1))
+            x = reg.get(v)
+            if not (x and x[0] == "x"):
+                errs.append(f"{ln}: exponential of {x}")
+            reg[v] = ("p",) + (x[1:] if x else (None, None))
+            continue
+        m = re.match(r"v_cmp_gt_i32 vcc, (\d+), %(\d+)$", ln)
+        if m:
+            reg["vcc"] = ("mask", int(m.group(2)) - 7)
+            continue
+        m = re.match(r"v_cndmask_b32_e64 v(\d+), v(\d+), 0, vcc", ln)
+        if m:
+            x = reg.get(int(m.group(1)))
+            if not (x and x[0] == "p" and reg.get("vcc") == ("mask", x[2])):
+                errs.append(f"{ln}: masks {x} with {reg.get('vcc')}")
+            continue
+        m = re.match(r"v_mul_f32 v(\d+), v(\d+), v(\d+)", ln)
+        if m:
+            d, s_, p_ = (int(g) for g in m.groups())
+            x, y = reg.get(s_), reg.get(p_)
+            if not (x and y and x[0] == "p" and y[0] == "P" and y[3] == 7 and x[1:] == y[1:3]):
+                errs.append(f"{ln}: dS from {x} and {y}")
+            reg[d] = ("dS",) + (x[1:] if x else (None, None))
+            continue
+        m = re.match(r"v_cvt_pk_bf16_f32 v(\d+), v(\d+), v(\d+)", ln)
+        if m:
+            d, s0, s1 = (int(g) for g in m.groups())
+            x0, x1 = reg.get(s0), reg.get(s1)
+            if not (x0 and x0[0] == "dS" and x1 == x0):
+                errs.append(f"{ln}: packs {x0} and {x1}")
+            reg[d] = ("dSk", x0[1] if x0 else None, x0[2] if x0 else None, (_set_of(d)[2]) // 8)
+            continue
+        errs.append(f"{ln}: not part of the stream's vocabulary")
+    for qg in range(2):
+        for db in range(4):
+            want = [(lb, mg) for lb in range(4) for mg in range(2)]
+            if acc.get((qg, db), []) != want:
+                errs.append(f"dQ^T ({qg}, {db}): contributions {acc.get((qg, db))}, want {want}")
+    return errs
+
+
+def _dq128_variants():
+    return _variants(_gen("gen_dq128_asm").render(), "TTFA_DQ128_STAGE_ASM", "dq128")
+
+
+def test_dq128_committed_file_is_the_generator_output():
+    gen = _gen("gen_dq128_asm")
+    assert (CSRC / "dq128_stage.inc").read_text() == gen.render(), \
+        "dq128_stage.inc is stale: run python tinytrain_amd/csrc/gen_dq128_asm.py"
+
+
+@pytest.mark.parametrize("name", ["FULL", "MASKED"])
+def test_dq128_stream_rules_counts_and_dataflow(name):
+    var = _dq128_variants()
+    assert set(var) == {"FULL", "MASKED"}
+    lines = var[name]
+    _check_stream(lines)
+    count = lambda p: sum(1 for ln in lines if ln.startswith(p))
+    assert count("v_mfma") == 8 * 24                  # 8 items: S^T, dP^T 16, dQ^T 8
+    assert count("ds_read_b128") == 4 * 16            # K and V rows, once per key block
+    assert count("ds_read_b64_tr_b16") == 4 * 16      # K^T halves, once per key block
+    assert count("v_exp_f32") == 8 * 16
+    assert count("v_cmp_gt_i32") == (0 if name == "FULL" else 8 * 16)
+    assert count("v_cvt_pk_bf16_f32") == 8 * 8
+    assert _dataflow_dq128(lines) == []
+
+
+def test_dq128_dataflow_check_catches_a_wrong_row_group():
+    """Swapping one product's Q fragment for the other row group's fails the replay, and
+    so does dropping one K^T read."""
+    lines = _dq128_variants()["FULL"]
+    assert _dataflow_dq128(lines) == []
+    i = next(k for k, ln in enumerate(lines) if ln.startswith("v_mfma") and ", a[128:131], " in ln)
+    swapped = lines[:i] + [lines[i].replace("a[128:131]", "a[160:163]")] + lines[i + 1:]
+    assert _dataflow_dq128(swapped) != []
+    j = next(k for k, ln in enumerate(lines) if ln.startswith("ds_read_b64_tr_b16"))
+    assert _dataflow_dq128(lines[:j] + lines[j + 1:]) != []

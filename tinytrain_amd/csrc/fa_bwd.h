@@ -42,6 +42,14 @@ __global__ void fa_bwd_dq_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf16
                                           const float *__restrict__ LSE, float *__restrict__ Delta,
                                           bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
                                           float scale_log2, float scale, int paired);
+// D = 128 dQ pass over 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): for launches
+// whose 256-row pairs fill the resident workgroup slots.
+__global__ void fa_bwd_dq_wide_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                           const bf16 *__restrict__ V, const bf16 *__restrict__ O,
+                                           const bf16 *__restrict__ dO,
+                                           const float *__restrict__ LSE, float *__restrict__ Delta,
+                                           bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
+                                           float scale_log2, float scale, int paired);
 template <int D>
 __global__ void fa_bwd_dkdv_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
                                         const bf16 *__restrict__ V, const bf16 *__restrict__ dO,
@@ -74,6 +82,8 @@ __global__ void fa_bwd_dkdv_bf16_kernel<128>(const bf16 *__restrict__ Q, const b
 constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
 constexpr int kDkv128LdsBytes = 2 * (2 * 128 * 128 * 2 + 2 * 128 * 4);
 constexpr int kDq64LdsBytes = 2 * 2 * 128 * 64 * 2;
+// D = 128 dQ pass: two 128-key stages of K and V tiles (workgroups of 256 query rows).
+constexpr int kDq128LdsBytes = 2 * 2 * 128 * 128 * 2;
 
 // Raises KERN's dynamic-LDS limit (needed above 64 KiB) once per device: later launches,
 // including launches under stream capture, make no attribute call.

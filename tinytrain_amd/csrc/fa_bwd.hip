@@ -587,6 +587,22 @@ template <int D>
 static hipError_t launch_dq(const void *q, const void *k, const void *v, const void *o,
                             const void *dout, const float *lse, float *delta, void *dq, int B,
                             int Hq, int Hkv, int T, float scale, hipStream_t stream) {
+  if constexpr (D == 128) {
+    // 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): half the LDS and L2 bytes per
+    // product, but half the workgroups, so only where its pairs fill the resident slots.
+    const int n_wide = (T + 255) / 256;
+    hipError_t e = allow_lds<fa_bwd_dq_wide_bf16_kernel>(kDq128LdsBytes);  // before the
+    if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
+    const int slots = resident_slots<fa_bwd_dq_wide_bf16_kernel>(256, kDq128LdsBytes);
+    if (sched_items(true, n_wide, B, Hq) >= slots) {
+      const bool paired = use_pairs(n_wide, B, Hq, slots);
+      const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
+      fa_bwd_dq_wide_bf16_kernel<<<grid, block, kDq128LdsBytes, stream>>>(
+          (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (const bf16 *)o, (const bf16 *)dout,
+          lse, delta, (bf16 *)dq, B, Hq, Hkv, T, scale * kLog2e, scale, (int)paired);
+      return hipGetLastError();
+    }
+  }
   const int n_tiles = (T + DqTile<D>::BM - 1) / DqTile<D>::BM;
   constexpr size_t lds = D == 64 ? kDq64LdsBytes : DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_bf16_kernel<D>;

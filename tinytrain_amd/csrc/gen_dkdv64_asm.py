@@ -288,7 +288,8 @@ def hoist_lds(ops, lead=LDS_LEAD):
     """Places the LDS reads of an op list.  Each read goes LDS_LEAD MFMAs ahead of its
     first consumer (the first later instruction that uses a register it fills), or as
     early as the registers allow if that is later: after the last instruction that still
-    uses their previous value.  Reads placed at the same point keep consumer order."""
+    uses their previous value, and after the writer of any register it reads (an address).
+    Reads placed at the same point keep consumer order."""
     core = [op for op in ops if op.kind != 'lds']
     index = {id(op): i for i, op in enumerate(core)}
     placed = []  # (position in core: insert before core[pos], consumer index, seq, op)
@@ -297,11 +298,11 @@ def hoist_lds(ops, lead=LDS_LEAD):
         if op.kind != 'lds':
             n_before += 1
             continue
-        dst = set(op.writes)
+        dst, src = set(op.writes), set(op.reads)
         legal = 0
         for i in range(n_before - 1, -1, -1):
             c = core[i]
-            if dst & (set(c.reads) | set(c.writes)):
+            if dst & (set(c.reads) | set(c.writes)) or src & set(c.writes):
                 legal = i + 1
                 if c.kind == 'mfma' and dst & set(c.reads):
                     # WAR_MFMAS more MFMAs must issue first
