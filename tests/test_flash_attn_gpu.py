@@ -108,8 +108,8 @@ def test_config_parity(name):
     (2, 32, 4, 2048),
 ])
 def test_wide_dq_pass(B, H, H_kv, T):
-    """Shapes whose 256-row pairs fill the 256 resident workgroup slots of an MI355X, so
-    the dQ pass runs its 64-rows-per-wave kernel (the smaller shapes above take the
+    """Shapes with T > 1792 whose 256-row pairs fill the 256 resident workgroup slots of
+    an MI355X, so the dQ pass runs its 64-rows-per-wave kernel (the smaller shapes above take the
     128-row one); two (batch, kv-head) groups checked against the oracle."""
     D = 128
     announce(f"wide dQ B={B} H={H} Hkv={H_kv} T={T} D={D}")

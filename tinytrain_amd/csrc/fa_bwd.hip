@@ -589,12 +589,14 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
                             int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   if constexpr (D == 128) {
     // 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): half the LDS and L2 bytes per
-    // product, but half the workgroups, so only where its pairs fill the resident slots.
+    // product, but half the workgroups and a longer prologue per workgroup, so only where
+    // its pairs fill the resident slots and carry at least 18 key stages each (T > 1792;
+    // measured slower at T = 512 and 1024, faster from T = 2000 up).
     const int n_wide = (T + 255) / 256;
     hipError_t e = allow_lds<fa_bwd_dq_wide_bf16_kernel>(kDq128LdsBytes);  // before the
     if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
     const int slots = resident_slots<fa_bwd_dq_wide_bf16_kernel>(256, kDq128LdsBytes);
-    if (sched_items(true, n_wide, B, Hq) >= slots) {
+    if (n_wide >= 8 && sched_items(true, n_wide, B, Hq) >= slots) {
       const bool paired = use_pairs(n_wide, B, Hq, slots);
       const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
       fa_bwd_dq_wide_bf16_kernel<<<grid, block, kDq128LdsBytes, stream>>>(
