@@ -539,3 +539,36 @@ def test_dq128_dataflow_check_catches_a_wrong_row_group():
     assert _dataflow_dq128(swapped) != []
     j = next(k for k, ln in enumerate(lines) if ln.startswith("ds_read_b64_tr_b16"))
     assert _dataflow_dq128(lines[:j] + lines[j + 1:]) != []
+
+
+# ---- D = 128 forward stage (fwd128_stage.inc) ------------------------------------------
+
+
+def test_fwd128_committed_file_is_the_generator_output():
+    gen = _gen("gen_fwd128_asm")
+    assert (CSRC / "fwd128_stage.inc").read_text() == gen.render(), \
+        "fwd128_stage.inc is stale: run python tinytrain_amd/csrc/gen_fwd128_asm.py"
+
+
+@pytest.mark.parametrize("name", ["FULL", "MASKED"])
+def test_fwd128_stream_rules_and_counts(name):
+    """Waits, hazard padding and instruction counts of the forward stream; the lazy
+    rescale blocks are checked as if taken (the conservative reading: the padding after a
+    skipped block is then only longer than needed)."""
+    var = _variants(_gen("gen_fwd128_asm").render(), "TTFA_FWD128_STAGE_ASM", "fw")
+    assert set(var) == {"FULL", "MASKED"}
+    lines = var[name]
+    _check_stream(lines)
+    count = lambda p: sum(1 for ln in lines if ln.startswith(p))
+    assert count("v_mfma") == 8 * 16                  # 8 items: S^T 8, PV 8
+    assert count("ds_read_b128") == 4 * 8             # K rows, once per key block
+    assert count("ds_read_b64_tr_b16") == 4 * 16      # V^T halves, once per key block
+    assert count("v_exp_f32") == 8 * (16 + 1)         # P^T, and the rescale factor
+    assert count(".Lfr_") == 8                        # one lazy-rescale block per item
+    assert count("v_permlane32_swap_b32") == 8        # the row max across the lane halves
+    assert count("v_cmp_gt_i32") == (0 if name == "FULL" else 8 * 16)
+    assert count("v_cvt_pk_bf16_f32") == 8 * 8
+    # every permlane reads its sources 2 wait states after they were written
+    for i, ln in enumerate(lines):
+        if ln.startswith("v_permlane32_swap_b32"):
+            assert lines[i - 1] == "s_nop 1", lines[i - 2:i + 1]

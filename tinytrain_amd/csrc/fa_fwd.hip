@@ -28,6 +28,7 @@
 // most tiles skip the rescale entirely.  The stored LSE is converted back to natural
 // log.  Tiles entirely above the diagonal are never loaded; only tiles that cross the
 // diagonal or the ragged end of T run the masked body.
+#include "fa_bwd.h"  // allow_lds
 #include "fa_common.h"
 #include "fa_kernels.h"
 
@@ -297,11 +298,35 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_varlen_bf16_kernel(
   fwd_rows<D>(lds, hd, qt, scale_log2, min(n_kt, (qt + 1) * (P::BM / P::BN)), wmax);
 }
 
+// D = 128 forward over 256-row tiles, 64 rows per wave (fa_fwd128.hip).
+__global__ void fa_fwd_wide_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
+                                        const bf16 *__restrict__ V, bf16 *__restrict__ O,
+                                        float *__restrict__ LSE, int B, int Hq, int Hkv, int T,
+                                        float scale_log2, int paired);
+constexpr int kFwd128LdsBytes = 2 * 2 * 128 * 128 * 2;  // two 128-key stages of K and V
+
 hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
                            int B, int Hq, int Hkv, int T, int D, float scale,
                            hipStream_t stream) {
   const int n_tiles = (T + FwdTile<64>::BM - 1) / FwdTile<64>::BM;
   const float sl2 = scale * kLog2e;
+  if (D == 128) {
+    // 256-row tiles, 64 rows per wave: half the LDS bytes per product, but half the
+    // workgroups and a longer prologue, so only where its pairs fill the resident slots
+    // and carry at least 18 key stages each (T > 1792), as for the wide dQ pass
+    const int n_wide = (T + 255) / 256;
+    hipError_t e = allow_lds<fa_fwd_wide_bf16_kernel>(kFwd128LdsBytes);  // before the
+    if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
+    const int slots = resident_slots<fa_fwd_wide_bf16_kernel>(256, kFwd128LdsBytes);
+    if (n_wide >= 8 && sched_items(true, n_wide, B, Hq) >= slots) {
+      const bool paired = use_pairs(n_wide, B, Hq, slots);
+      const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
+      fa_fwd_wide_bf16_kernel<<<grid, block, kFwd128LdsBytes, stream>>>(
+          (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o, lse, B, Hq, Hkv, T, sl2,
+          (int)paired);
+      return hipGetLastError();
+    }
+  }
   auto go = [&](auto kern, int slots) {
     const bool paired = use_pairs(n_tiles, B, Hq, slots);
     const dim3 grid((unsigned)sched_items(paired, n_tiles, B, Hq)), block(256);
