@@ -572,3 +572,137 @@ def test_fwd128_stream_rules_and_counts(name):
     for i, ln in enumerate(lines):
         if ln.startswith("v_permlane32_swap_b32"):
             assert lines[i - 1] == "s_nop 1", lines[i - 2:i + 1]
+
+
+def _dataflow_fwd128(lines):
+    """Replays one emitted forward variant on tags (as for the dQ stream): K rows and V^T
+    fragments by block, S^T chains by (block, row group, k-step), the row max, P^T and its
+    packing, the row-group operands of every softmax step, and each O^T accumulator's
+    contributions."""
+    reg, acc, errs = {}, {}, []
+    cur = None  # (block, row group) whose softmax runs
+    for ln in lines:
+        if ln.startswith(("s_nop", "s_waitcnt", ".Lfr_")):
+            continue
+        m = re.match(r"v_(mov|xor)_b32 v(\d+), (?:(\d+), )?(%\d+|0xff800000)$", ln)
+        if m and int(m.group(2)) >= 96:
+            reg[int(m.group(2))] = ("addr", m.group(4), int(m.group(3) or 0))
+            continue
+        m = re.match(r"ds_read_b128 (\S+), v(\d+) offset:(\d+)", ln)
+        if m:
+            a, off = int(m.group(2)), int(m.group(3))
+            kk = a - 96
+            if reg.get(a) != ("addr", "%4", 32 * kk) or off % 8192 or off >= 32768:
+                errs.append(f"{ln}: K row read from {reg.get(a)} at {off}")
+            for v in _vrange(m.group(1)):
+                reg[v] = ("k", off // 8192, kk)
+            continue
+        m = re.match(r"ds_read_b64_tr_b16 (\S+), v(\d+) offset:(\d+)", ln)
+        if m:
+            a, off = int(m.group(2)), int(m.group(3))
+            i = a - 104
+            db, h = divmod(i, 2)
+            row = (off - 32768) // 256
+            if reg.get(a) != ("addr", "%5", 32 * i) or off < 32768 or (row % 16) // 8 != h:
+                errs.append(f"{ln}: V^T read from {reg.get(a)} at {off}")
+            for v in _vrange(m.group(1)):
+                reg[v] = ("vt", row // 32, (row % 32) // 16, db, h)
+            continue
+        m = re.match(r"v_mfma_f32_32x32x16_bf16 (\S+), (\S+), (\S+), (\S+)", ln)
+        if m:
+            d, a, b, c = m.groups()
+            if d.startswith("a"):  # O^T += V^T P^T
+                qg, db = divmod(_agpr_base(d), 64)
+                db //= 16
+                A = [reg.get(v) for v in _vrange(a)]
+                B = [reg.get(v) for v in _vrange(b)]
+                if None in A or any(x[0] != "vt" or x[3] != db for x in A) \
+                        or [x[4] for x in A] != [0, 0, 1, 1] or len({x[1:3] for x in A}) != 1:
+                    errs.append(f"{ln}: A operand {A}")
+                    continue
+                lb, mg = A[0][1], A[0][2]
+                if any(x != ("pk", lb, qg, mg) for x in B):
+                    errs.append(f"{ln}: B operand {B}, want {('pk', lb, qg, mg)}")
+                acc.setdefault((qg, db), []).append((lb, mg))
+                continue
+            D_, A = _vrange(d), [reg.get(v) for v in _vrange(a)]
+            if None in A or any(x[0] != "k" or x != A[0] for x in A):
+                errs.append(f"{ln}: A operand {A}")
+                continue
+            _, lb, kk = A[0]
+            qg, bkk = divmod((_agpr_base(b) - 128) // 4, 8)
+            if bkk != kk:
+                errs.append(f"{ln}: Q fragment k-step {bkk} for K k-step {kk}")
+            want = "0" if kk == 0 else None
+            if kk == 0 and c != "0":
+                errs.append(f"{ln}: chain does not start at 0")
+            if kk > 0 and any(reg.get(v) != ("s", lb, qg, kk - 1) for v in D_):
+                errs.append(f"{ln}: C holds {reg.get(D_[0])}, want {('s', lb, qg, kk - 1)}")
+            for v in D_:
+                reg[v] = ("s", lb, qg, kk)
+            continue
+        m = re.match(r"v_maximum3_f32 v(\d+), v(\d+), v(\d+), v(\d+)", ln)
+        if m:
+            srcs = [reg.get(int(x)) for x in m.groups()[1:]]
+            items = {x[1:3] for x in srcs if x and x[0] in ("s", "mx")}
+            if any(x is None or x[0] not in ("s", "mx") or (x[0] == "s" and x[3] != 7) for x in srcs) \
+                    or len(items) != 1:
+                errs.append(f"{ln}: max over {srcs}")
+            else:
+                cur = items.pop()
+            reg[int(m.group(1))] = ("mx",) + (cur if cur else (None, None))
+            continue
+        m = re.match(r"v_fma_f32 v(\d+), v(\d+), %6, -%(\d+)$", ln)
+        if m:
+            v, qg = int(m.group(1)), int(m.group(3))
+            x = reg.get(v)
+            if not (x and x[0] == "s" and x[3] == 7 and x[2] == qg):
+                errs.append(f"{ln}: exponent of {x} with row group {qg}'s max")
+            reg[v] = ("x", x[1], x[2]) if x else None
+            continue
+        m = re.match(r"v_exp_f32 v(\d+), v(\d+)$", ln)
+        if m:
+            v = int(m.group(1))
+            x = reg.get(v)
+            if v < 32:
+                if not (x and x[0] == "x"):
+                    errs.append(f"{ln}: exponential of {x}")
+                reg[v] = ("p", x[1], x[2]) if x else None
+            continue
+        m = re.match(r"v_add_f32 v(\d+), v(\d+), v(\d+)$", ln)
+        if m and int(m.group(2)) < 32:
+            x = reg.get(int(m.group(2)))
+            if not (x and x[0] == "p"):
+                errs.append(f"{ln}: row sum of {x}")
+            continue
+        m = re.match(r"v_add_f32 %(\d+), %(\d+), v(\d+)$", ln)
+        if m:
+            if not (cur and int(m.group(1)) == 2 + cur[1]):
+                errs.append(f"{ln}: row sum into row group {int(m.group(1)) - 2}, item {cur}")
+            continue
+        m = re.match(r"v_cvt_pk_bf16_f32 v(\d+), v(\d+), v(\d+)", ln)
+        if m:
+            d, s0, s1 = (int(g) for g in m.groups())
+            x0, x1 = reg.get(s0), reg.get(s1)
+            if not (x0 and x0[0] == "p" and x1 == x0):
+                errs.append(f"{ln}: packs {x0} and {x1}")
+            reg[d] = ("pk", x0[1], x0[2], (d % 16) // 8) if x0 else None
+            continue
+        m = re.match(r"v_add_f32 v\d+, 8\.0, %(\d+)$", ln)
+        if m and not (cur and int(m.group(1)) == cur[1]):
+            errs.append(f"{ln}: rescale test of row group {m.group(1)}, item {cur}")
+    for qg in range(2):
+        for db in range(4):
+            want = [(lb, mg) for lb in range(4) for mg in range(2)]
+            if acc.get((qg, db), []) != want:
+                errs.append(f"O^T ({qg}, {db}): contributions {acc.get((qg, db))}, want {want}")
+    return errs
+
+
+@pytest.mark.parametrize("name", ["FULL", "MASKED"])
+def test_fwd128_dataflow(name):
+    lines = _variants(_gen("gen_fwd128_asm").render(), "TTFA_FWD128_STAGE_ASM", "fw")[name]
+    assert _dataflow_fwd128(lines) == []
+    # a product with the other row group's Q fragment fails the replay
+    i = next(k for k, ln in enumerate(lines) if ln.startswith("v_mfma") and ", a[128:131], " in ln)
+    assert _dataflow_fwd128(lines[:i] + [lines[i].replace("a[128:131]", "a[160:163]")] + lines[i + 1:]) != []
