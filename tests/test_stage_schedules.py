@@ -363,7 +363,8 @@ def test_d128_dataflow_check_catches_a_misplaced_read():
 # v[128+16m+4db] K^T fragments; v[160+kk] row-read addresses (%0 ^ 32kk), v[168+i]
 # transposed-read addresses (%1 ^ 32i, i = 2db + h).  AGPRs: a[64qg+16db:+15] dQ^T
 # accumulators, a[128+32qg+4kk:+3] Q fragments, a[192+32qg+4kk:+3] dO fragments.
-# Operands: %2 scale, %3+qg -LSE, %5+qg -Delta, %7+qg mask bound.  LDS stage: K rows at
+# Operands: %2 scale, %3+qg -LSE, %7+qg mask bound, %10+qg the -Delta blocks that start
+# the dP^T chains.  LDS stage: K rows at
 # 0, V rows at +32768, 256 bytes a row, 32-key blocks of 8192 bytes.
 
 
@@ -408,10 +409,6 @@ def _dataflow_dq128(lines):
             for v in dst:
                 reg[v] = ("kt", row // 32, (row % 32) // 16, db, h)
             continue
-        m = re.match(r"v_mov_b32 v(\d+), %(\d+)$", ln)
-        if m:
-            reg[int(m.group(1))] = ("ndelta", int(m.group(2)) - 5)
-            continue
         m = re.match(r"v_mfma_f32_32x32x16_bf16 (\S+), (\S+), (\S+), (\S+)", ln)
         if m:
             d, a, b, c = m.groups()
@@ -444,8 +441,11 @@ def _dataflow_dq128(lines):
             if kk == 0 and tensor == 0:
                 if c != "0":
                     errs.append(f"{ln}: S^T chain does not start at 0")
+            elif kk == 0:  # the dP^T chain starts from the row group's -Delta block
+                if c != f"%{10 + qg}":
+                    errs.append(f"{ln}: dP^T chain of row group {qg} starts from {c}")
             else:
-                want = ("ndelta", qg) if kk == 0 else (name, lb, qg, kk - 1)
+                want = (name, lb, qg, kk - 1)
                 bad = [v for v in D_ if reg.get(v) != want]
                 if bad:
                     errs.append(f"{ln}: C register v{bad[0]} holds {reg.get(bad[0])}, want {want}")

@@ -31,15 +31,16 @@ struct DqRows128 {
 // lane's LDS byte addresses of the stage's k-step 0 row read and (column block 0, half
 // 0) transposed read; nlse, ndelta, dm: -LSE*log2(e), -Delta and the mask bound of the
 // lane's row in each row group; mode 0: every key visible to both row groups, 1: every
-// item masked (a key is dropped when its offset in the stage minus 4lg exceeds dm).
+// item masked (a key is dropped when its offset in the stage minus 4lg exceeds dm); ndb:
+// -Delta in all 16 registers per row group, the dP^T chains' start value.
 #define TTFA_DQ128_OPERANDS                                                              \
   :                                                                                      \
   : "v"(aR0), "v"(aT0), "s"(scale_log2), "v"(nlse[0]), "v"(nlse[1]), "v"(ndelta[0]),     \
-    "v"(ndelta[1]), "v"(dm[0]), "v"(dm[1]), "s"(mode)                                    \
+    "v"(ndelta[1]), "v"(dm[0]), "v"(dm[1]), "s"(mode), "v"(ndb[0]), "v"(ndb[1])          \
   : TTFA_DQ128_STAGE_CLOBBERS, "memory"
 __device__ __forceinline__ void dq128_stage(uint32_t aR0, uint32_t aT0, float scale_log2,
                                             const float (&nlse)[2], const float (&ndelta)[2],
-                                            const int (&dm)[2], int mode) {
+                                            const int (&dm)[2], int mode, const f32x16 (&ndb)[2]) {
   asm volatile(TTFA_DQ128_STAGE_ASM TTFA_DQ128_OPERANDS);
 }
 #undef TTFA_DQ128_OPERANDS
@@ -142,6 +143,11 @@ __device__ __forceinline__ void dq_rows256(bf16 *lds, const DqRows128 &hd, int q
     dm[qg] = min(qrow, T - 1) - 4 * lg;
   }
   dq128_init(qf, dof);
+  f32x16 ndb[2];
+#pragma unroll
+  for (int qg = 0; qg < 2; ++qg)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ndb[qg][r] = ndelta[qg];
   // the lane's LDS addresses of the k-step 0 row read and the (column block 0, half 0)
   // transposed read in stage 0; the stream derives the others (the XOR of swz_rows128)
   const uint32_t base = lds_addr(lds);
@@ -163,7 +169,7 @@ __device__ __forceinline__ void dq_rows256(bf16 *lds, const DqRows128 &hd, int q
       const int mode = __builtin_amdgcn_readfirstlane(k0 + BN - 1 <= q0u && k0 + BN <= T ? 0 : 1);
       const uint32_t so = (j & 1) * STAGE_BYTES;
       const int dmj[2] = {dm[0] - k0, dm[1] - k0};
-      dq128_stage(aR0 + so, aT0 + so, scale_log2, nlse, ndelta, dmj, mode);
+      dq128_stage(aR0 + so, aT0 + so, scale_log2, nlse, ndelta, dmj, mode, ndb);
     }
     wait_vm_all();  // stage j+1 is in LDS before any wave passes the barrier
     __syncthreads();

@@ -1,5 +1,5 @@
 // Causal GQA FlashAttention forward at D = 128 over 256-row tiles (bf16 in, fp32
-// accumulate, gfx950): the reference's fwd kernel (kernels/flash_attn.py:18-68).  A
+// accumulate, gfx950): the reference's fwd_kernel (kernels/flash_attn.py:12-67).  A
 // workgroup takes 256 query rows of one (batch, head), 4 waves x 64 rows: each wave keeps
 // the Q fragments and O^T accumulators of its two 32-row groups in fixed AGPRs.  The keys
 // stream through LDS in 128-key stages (K and V tiles, double-buffered: 128 KB), and each

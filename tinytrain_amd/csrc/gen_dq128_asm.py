@@ -31,7 +31,9 @@ Operands: %0 the lane's LDS byte address of the k-step 0 row read of key block 0
 tile; the V tile at +32768), %1 that of its transposed read for column block 0, half 0;
 %2 the SGPR scale*log2(e); %3, %4 -LSE*log2(e) of the lane's row in each row group;
 %5, %6 -Delta; %7, %8 the mask bounds (a key is masked when its offset in the stage minus
-4lg exceeds the bound); %9 the SGPR mode (0: FULL, 1: MASKED).
+4lg exceeds the bound); %9 the SGPR mode (0: FULL, 1: MASKED); %10, %11 16-register
+blocks holding -Delta in every register (the C operand of each row group's first dP^T
+product, so no item spends moves on its start value).
 The tiles use swz_rows128 (row bits 0-3 XOR all four chunk bits), so with the stage
 base 256-byte aligned the row read of k-step kk is at %40 ^ 32kk and the transposed read
 of (db, h) at (%41 ^ (64db + 32h)) + 2048h; the key blocks (+8192 bytes) and key row
@@ -80,6 +82,7 @@ OP_NLSE = [3, 4]
 OP_NDELTA = [5, 6]
 OP_DM = [7, 8]
 OP_MODE = 9
+OP_NDB = [10, 11]  # 16-register blocks of -Delta (the dP^T chains' start), per row group
 
 
 def addresses():
@@ -121,11 +124,6 @@ def l_kt_all(lb):
     return [l_kt(lb, m, db, h) for m in range(2) for db in range(DB) for h in range(2)]
 
 
-def init_dp(rs, qg):
-    return [Op(f'v_mov_b32 v{P[rs] + r}, %{OP_NDELTA[qg]}', 'valu', writes=[f'v{P[rs] + r}'])
-            for r in range(16)]
-
-
 def m_s(rs, qg, kk):
     src_c = '0' if kk == 0 else vt(S[rs], 16)
     reads = vr(KR + 4 * kk, 4) + ([] if kk == 0 else vr(S[rs], 16))
@@ -134,8 +132,10 @@ def m_s(rs, qg, kk):
 
 
 def m_p(rs, qg, kk):
-    return Op(f'v_mfma_f32_32x32x16_bf16 {vt(P[rs], 16)}, {vt(VR + 4 * kk, 4)}, {A_DF[qg][kk]}, {vt(P[rs], 16)}',
-              'mfma', reads=vr(P[rs], 16) + vr(VR + 4 * kk, 4), writes=vr(P[rs], 16))
+    src_c = f'%{OP_NDB[qg]}' if kk == 0 else vt(P[rs], 16)
+    reads = vr(VR + 4 * kk, 4) + ([src_c] if kk == 0 else vr(P[rs], 16))
+    return Op(f'v_mfma_f32_32x32x16_bf16 {vt(P[rs], 16)}, {vt(VR + 4 * kk, 4)}, {A_DF[qg][kk]}, {src_c}',
+              'mfma', reads=reads, writes=vr(P[rs], 16))
 
 
 def m_dq(rs, qg, m, db):
@@ -191,7 +191,6 @@ def schedule_stage(masked):
     n = len(items)
     ops = addresses()
     ops += l_rows(0)
-    ops += init_dp(0, 0)
     ops += sd_products(0, 0)
     for i in range(n):
         b, qg = items[i]
@@ -204,7 +203,6 @@ def schedule_stage(masked):
             nb, nqg = items[i + 1]
             if nqg == 0:  # a new key block: its K/V rows replace block b's
                 mf.append(('L', l_rows(nb)))
-            mf.append(('V', init_dp(os_, nqg)))
             mf += sd_products(os_, nqg)
         if qg == 0:  # block b's K^T fragments, for the dQ^T products of rounds i+1, i+2
             mf.append(('L', l_kt_all(b)))
