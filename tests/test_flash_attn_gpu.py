@@ -102,17 +102,18 @@ def test_config_parity(name):
             assert_close_abs(nm, got, want, tol, f"[{name} vs eager fp32]")
 
 
-# ------------------------------------------------- the 256-row dQ pass at D = 128
+# ------------------------------------------------- the 256-row forward and dQ pass at D = 128
 @pytest.mark.parametrize("B, H, H_kv, T", [
     (1, 64, 8, 2000),   # T ragged to the 128-key stages and 256-row tiles
     (2, 32, 4, 2048),
+    (1, 64, 64, 1810),  # G = 1; three of the last tile's four waves hold no row inside T
 ])
-def test_wide_dq_pass(B, H, H_kv, T):
+def test_wide_d128_kernels(B, H, H_kv, T):
     """Shapes with T > 1792 whose 256-row pairs fill the 256 resident workgroup slots of
-    an MI355X, so the dQ pass runs its 64-rows-per-wave kernel (the smaller shapes above take the
+    an MI355X, so the forward and the dQ pass run their 64-rows-per-wave kernels (the smaller shapes above take the
     128-row one); two (batch, kv-head) groups checked against the oracle."""
     D = 128
-    announce(f"wide dQ B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    announce(f"wide D=128 kernels B={B} H={H} Hkv={H_kv} T={T} D={D}")
     q, k, v, do = make_custom(B, H, H_kv, T, D, torch.bfloat16, seed=3)
     o, M, dq, dk, dv = _run(q, k, v, do)
     G = H // H_kv
