@@ -8,8 +8,9 @@ S^T = K Q^T) and O^T accumulators stay in fixed AGPRs.  Each K row fragment and 
 fragment read from LDS feeds one product per row group: half the LDS bytes per product of
 a 32-row wave.  The work items of a stage are (32-key block b, row group qg), in the order
 (b0,q0), (b0,q1), (b1,q0), ...; an item is 8 S^T products, the online softmax on the
-VALU (row max over the item's 32 keys, a lazy rescale of O and l when the max grows by
-more than 2^8, P^T = exp2(S^T * scale*log2e - m), the row sum, P^T packed to bf16) and 8
+VALU (row max over the item's 32 keys as a maximum3 tree, a lazy rescale of O and l
+when the max grows by more than 2^8, P^T = exp2(S^T * scale*log2e - m), the row sum in
+four partial sums, P^T packed to bf16) and 8
 PV products (O^T += V^T P^T, 2 key row groups m x 4 column blocks db).  As in the
 backward streams (gen_dkdv64_asm.py, whose emitter and LDS placement this reuses), the
 items form a software pipeline: round i runs item i's VALU work under item i-1's PV
@@ -20,8 +21,9 @@ Register map (fixed; the statement clobbers v[0:121]):
   block into registers 8m..8m+3), v[16:31] set 1; v[32+4kk] K row fragments of the
   current block; v[64+16m+4db] V^T fragments (key row group m, column block db);
   v[96+kk] the LDS addresses of the K row reads of k-step kk, v[104+2db+h] those of the
-  V^T reads (column block db, 8-row half h); v[112:121] temporaries (max, -inf, the
-  rescale factor).
+  V^T reads (column block db, 8-row half h); v[112:121] temporaries (the max tree's
+  partials, -inf, the rescale factor and new max, the rescale's O copies, the row sum's
+  four partial sums).
 AGPR state (fixed registers, written by TTFA_FWD128_INIT_ASM, read back by
 TTFA_FWD128_READ_ASM, held between the statements because every statement of the pass
 declares all AGPRs clobbered): a[64qg+16db : +15] the O^T accumulators (row group qg,
