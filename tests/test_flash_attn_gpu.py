@@ -107,6 +107,8 @@ def test_config_parity(name):
     (1, 64, 8, 2000),   # T ragged to the 128-key stages and 256-row tiles
     (2, 32, 4, 2048),
     (1, 64, 64, 1810),  # G = 1; three of the last tile's four waves hold no row inside T
+    (2, 48, 16, 2048),  # G = 3
+    (1, 68, 17, 2048),  # 17 KV groups: the schedule without the XCD grouping
 ])
 def test_wide_d128_kernels(B, H, H_kv, T):
     """Shapes with T > 1792 whose 256-row pairs fill the 256 resident workgroup slots of
