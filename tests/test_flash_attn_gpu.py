@@ -109,10 +109,12 @@ def test_config_parity(name):
     (1, 64, 64, 1810),  # G = 1; three of the last tile's four waves hold no row inside T
     (2, 48, 16, 2048),  # G = 3
     (1, 68, 17, 2048),  # 17 KV groups: the schedule without the XCD grouping
+    (1, 32, 8, 4000),   # T > 3840: the forward's 256-row kernel too, T ragged
 ])
 def test_wide_d128_kernels(B, H, H_kv, T):
     """Shapes with T > 1792 whose 256-row pairs fill the 256 resident workgroup slots of
-    an MI355X, so the forward and the dQ pass run their 64-rows-per-wave kernels (the smaller shapes above take the
+    an MI355X, so the dQ pass runs its 64-rows-per-wave kernel (and from T > 3840 the
+    forward too) (the smaller shapes above take the
     128-row one); two (batch, kv-head) groups checked against the oracle."""
     D = 128
     announce(f"wide D=128 kernels B={B} H={H} Hkv={H_kv} T={T} D={D}")

@@ -313,12 +313,13 @@ hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o,
   if (D == 128) {
     // 256-row tiles, 64 rows per wave: half the LDS bytes per product, but half the
     // workgroups and a longer prologue, so only where its pairs fill the resident slots
-    // and carry at least 18 key stages each (T > 1792), as for the wide dQ pass
+    // and T > 3840 (measured 5-7% slower at T = 2000-3072, even at 4096, 3-5% faster
+    // from 8192 up)
     const int n_wide = (T + 255) / 256;
     hipError_t e = allow_lds<fa_fwd_wide_bf16_kernel>(kFwd128LdsBytes);  // before the
     if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
     const int slots = resident_slots<fa_fwd_wide_bf16_kernel>(256, kFwd128LdsBytes);
-    if (n_wide >= 8 && sched_items(true, n_wide, B, Hq) >= slots) {
+    if (n_wide >= 16 && sched_items(true, n_wide, B, Hq) >= slots) {
       const bool paired = use_pairs(n_wide, B, Hq, slots);
       const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
       fa_fwd_wide_bf16_kernel<<<grid, block, kFwd128LdsBytes, stream>>>(
