@@ -21,8 +21,13 @@ from tinytrain_amd.model import ModelConfig, ModelForCausalLM
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-# hip's deviation from the fp32 logits, as a multiple of sdpa-bf16's own deviation
-MAX_RATIO = 1.15
+# hip's deviation from the fp32 logits, as a multiple of sdpa-bf16's own deviation.  The
+# mean is the tight bound: it measured 0.996-1.002 on every box.  The maximum is set by a
+# handful of logits; the compiled model around the (deterministic) attention kernels gives
+# different bf16 results on different boxes, and the ratio of the maxima measured
+# 0.97-1.02 on one box and 1.16 on another for the same code, so its bound leaves room
+# for that spread.  A wrong mask, scale or head map moves both far beyond these bounds.
+MAX_RATIO = 1.5
 MEAN_RATIO = 1.05
 
 
