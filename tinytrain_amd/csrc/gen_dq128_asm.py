@@ -8,8 +8,8 @@ row fragment and each K^T fragment read from LDS feeds one product per row group
 product costs half the LDS bytes of a 32-row wave (LDS delivery, not the matrix cores,
 bounds the 32-row form of this pass).  The work items of a stage are (32-key block b, row
 group qg), in the order (b0,q0), (b0,q1), (b1,q0), ...; an item is 16 S^T/dP^T products,
-~70 VALU operations (P^T = exp2(S^T * scale*log2e - LSE*log2e), dS^T = P^T (dP^T -
-Delta), packed to bf16) and 8 dQ^T products (dQ^T += K^T dS^T, 2 key row groups m x 4
+56 VALU operations (P^T = exp2(S^T * scale*log2e - LSE*log2e), dS^T = P^T (dP^T -
+Delta), packed to bf16; 32 more where masked) and 8 dQ^T products (dQ^T += K^T dS^T, 2 key row groups m x 4
 column blocks db).  As in the dK/dV passes (gen_dkdv64_asm.py, whose emitter and LDS
 placement this reuses), the items form a software pipeline: round i runs item i's VALU
 work under item i-1's dQ^T products and item i+1's S^T/dP^T products, in two alternating
