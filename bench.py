@@ -233,7 +233,7 @@ def _measure_sq(config: str, out: Path) -> int:
     on ``config`` (two rocprofv3 --pmc passes), summarised per kernel."""
     me = str(ROOT / "bench.py")
     work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
-            "--no-traffic", "--no-extras"]
+            "--settle-ms", "0", "--no-traffic", "--no-extras"]
     tmp = Path("/tmp") / f"ttfa_sq_{os.getpid()}"
     merged: dict = {}
     for i, ctrs in enumerate(SQ_PASSES):
@@ -290,6 +290,82 @@ def _measure_sq(config: str, out: Path) -> int:
     return 0
 
 
+# Two passes of memory-path counters (each within one pass's limits: at most 4 TCC,
+# 4 TCP, 2 TA, 2 TD, 2 GRBM).  TCC is the L2 of an XCD, TCP the CU's vector L1, TA/TD
+# its address and data units.
+L2_PASSES = (
+    ("TCC_HIT", "TCC_MISS", "TCC_EA0_RDREQ", "TCC_EA0_RDREQ_DRAM", "GRBM_GUI_ACTIVE"),
+    ("TA_TA_BUSY", "TA_ADDR_STALLED_BY_TC_CYCLES", "TCP_PENDING_STALL_CYCLES",
+     "TCP_TCC_READ_REQ", "TCP_TCC_READ_REQ_LATENCY", "TD_TD_BUSY", "TD_TC_STALL",
+     "GRBM_GUI_ACTIVE"),
+)
+
+
+def _measure_l2(config: str, out: Path) -> int:
+    """L2 hit rate, L2 read latency and the CU memory pipeline's busy / stall shares per
+    attention kernel on ``config`` (two rocprofv3 --pmc passes), summarised per kernel."""
+    me = str(ROOT / "bench.py")
+    work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
+            "--settle-ms", "0", "--no-traffic", "--no-extras"]
+    tmp = Path("/tmp") / f"ttfa_l2_{os.getpid()}"
+    merged: dict = {}
+    for i, ctrs in enumerate(L2_PASSES):
+        for name, vals in _pmc_multi(list(ctrs), [me, *work], tmp / f"pass{i}").items():
+            if "ttfa::" not in name:
+                continue
+            sym = name.split("ttfa::", 1)[1].split("(", 1)[0]
+            d = merged.setdefault(sym, {})
+            for c, v in vals.items():
+                d[c if c != "GRBM_GUI_ACTIVE" else f"GRBM_GUI_ACTIVE_{i}"] = v
+    cus, xcds = 256, 8  # GRBM_GUI_ACTIVE sums the 8 XCDs; one TA / TD / TCP per CU
+    rows, summary = [], {}
+    for sym, c in sorted(merged.items()):
+        gui0 = c.get("GRBM_GUI_ACTIVE_0", float("nan")) / xcds
+        gui1 = c.get("GRBM_GUI_ACTIVE_1", float("nan")) / xcds
+        hit, miss = c.get("TCC_HIT", 0.0), c.get("TCC_MISS", 0.0)
+        rdreq = max(c.get("TCC_EA0_RDREQ", 0.0), 1.0)
+        r = {
+            "l2_hit_rate": hit / max(hit + miss, 1.0),
+            "l2_requests": hit + miss,
+            "ea_read_requests": c.get("TCC_EA0_RDREQ", 0.0),
+            "ea_read_dram_share": c.get("TCC_EA0_RDREQ_DRAM", 0.0) / rdreq,
+            "l2_read_latency_cycles": c.get("TCP_TCC_READ_REQ_LATENCY", 0.0)
+            / max(c.get("TCP_TCC_READ_REQ", 0.0), 1.0),
+            "tcp_l2_read_requests": c.get("TCP_TCC_READ_REQ", 0.0),
+            "ta_busy": c.get("TA_TA_BUSY", 0.0) / (gui1 * cus),
+            "ta_addr_stalled_by_tc": c.get("TA_ADDR_STALLED_BY_TC_CYCLES", 0.0) / (gui1 * cus),
+            "tcp_pending_stall": c.get("TCP_PENDING_STALL_CYCLES", 0.0) / (gui1 * cus),
+            "td_busy": c.get("TD_TD_BUSY", 0.0) / (gui1 * cus),
+            "td_tc_stall": c.get("TD_TC_STALL", 0.0) / (gui1 * cus),
+            "gui_cycles_per_xcd": gui0,
+        }
+        summary[sym] = {k: round(v, 4) for k, v in r.items()}
+        rows.append(f"{sym:<34}{r['l2_hit_rate']:>8.3f}{r['ea_read_dram_share']:>8.3f}"
+                    f"{r['l2_read_latency_cycles']:>9.0f}{r['ta_busy']:>8.3f}"
+                    f"{r['ta_addr_stalled_by_tc']:>9.3f}{r['tcp_pending_stall']:>9.3f}"
+                    f"{r['td_busy']:>8.3f}{r['td_tc_stall']:>8.3f}")
+    lines = [
+        f"# L2 and CU memory-pipeline counters per attention kernel, workload {config} "
+        "(rocprofv3 --pmc, two passes)",
+        "# command: python bench.py --measure-l2 --config " + config,
+        "# passes:  rocprofv3 --pmc " + " ".join(L2_PASSES[0]) + " -- python bench.py " + " ".join(work),
+        "#          rocprofv3 --pmc " + " ".join(L2_PASSES[1]) + " -- python bench.py " + " ".join(work),
+        "# hit  = TCC_HIT / (TCC_HIT + TCC_MISS): L2 hit rate over all L2 requests",
+        "# dram = TCC_EA0_RDREQ_DRAM / TCC_EA0_RDREQ: share of L2 read misses sent to DRAM",
+        "# lat  = TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ: mean L2 read latency seen by a CU (cycles)",
+        "# ta, ta_tc, tcp_p, td, td_tc: TA_TA_BUSY, TA_ADDR_STALLED_BY_TC_CYCLES, "
+        "TCP_PENDING_STALL_CYCLES, TD_TD_BUSY, TD_TC_STALL",
+        "#   per CU, as shares of GRBM_GUI_ACTIVE / 8 (cycles per XCD)",
+        f"{'kernel':<34}{'hit':>8}{'dram':>8}{'lat':>9}{'ta':>8}{'ta_tc':>9}{'tcp_p':>9}{'td':>8}{'td_tc':>8}",
+        *rows,
+        "JSON " + json.dumps({"config": config, "kernels": summary}),
+    ]
+    out.parent.mkdir(parents=True, exist_ok=True)
+    out.write_text("\n".join(lines) + "\n")
+    print("\n".join(lines), flush=True)
+    return 0
+
+
 # bench.py's symbol stems -> the key of its per-kernel event average in the JSON line
 _EVENT_KEYS = (("fa_fwd_", ("passes", "fwd", "ms")), ("fa_bwd_dq_", ("passes", "bwd_dq_ms")),
                ("fa_bwd_dkdv_", ("passes", "bwd_dkdv_ms")), ("fa_bwd_f32_", ("passes", "bwd", "ms")))
@@ -326,6 +402,7 @@ def _measure_kernels(config: str, out: Path) -> int:
               f"see {log_path}", file=sys.stderr)
         return 1
     steps, warmup = line["steps"], line["warmup"]
+    warmup += (line.get("settle") or {}).get("steps", 0)  # settle steps precede the warmup
     durs: dict = {}
     for row in sorted(csv.DictReader(open(traces[0])), key=lambda r: int(r["Start_Timestamp"])):
         name = row["Kernel_Name"]
@@ -340,7 +417,7 @@ def _measure_kernels(config: str, out: Path) -> int:
         f"# command: python bench.py --measure-kernels --config {config}",
         "# which runs: cd /tmp && TMPDIR=/tmp rocprofv3 --kernel-trace --stats -d <out> -o run "
         f"--output-format csv -- python bench.py {' '.join(work)}",
-        f"# Dispatches per kernel: {warmup} warmup + {steps} timed steps (no event between "
+        f"# Dispatches per kernel: {warmup} settle + warmup + {steps} timed steps (no event between "
         f"launches) + {steps} breakdown steps (timing-only HIP events between launches) + "
         "hot-cache and graph-replay launches.",
         "# 'Calls'/'AverageNs' below are rocprofv3's own statistics over all of them.",
@@ -392,7 +469,7 @@ def _measure_traffic(config: str, out: Path) -> int:
     scaled by what the same counters read for a plain 256 MB device copy."""
     me = str(ROOT / "bench.py")
     work = ["--config", config, "--steps", "10", "--warmup", "2", "--cpu-budget", "0",
-            "--no-traffic", "--no-extras"]
+            "--settle-ms", "0", "--no-traffic", "--no-extras"]
     copy_mb = 256.0
     copy = ["--copy-probe-mb", str(copy_mb), "--steps", "10"]
     tmp = Path("/tmp") / f"ttfa_traffic_{os.getpid()}"
@@ -814,7 +891,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="C2", help="workload: C1..C5 (default C2)")
+    ap.add_argument("--settle-ms", type=float, default=600.0,
+                    help="before the warmup, run untimed steps for at least this much wall "
+                         "time, so the clocks and power state have reached their loaded "
+                         "level whatever --warmup says (reported as 'settle' in the line)")
+    ap.add_argument("--config", default="C2",
+                    help="workload: C1..C5, or REF112M (the reference model's attention shape); "
+                         "default C2")
     ap.add_argument("--sets", type=int, default=0,
                     help="input sets to rotate over (0: enough for > 512 MB)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
@@ -830,6 +913,9 @@ def main() -> int:
     ap.add_argument("--measure-sq", action="store_true",
                     help="run two rocprofv3 SQ-counter passes over --config (MFMA busy, VALU, "
                          "LDS bank conflicts) and write profiles/sq_counters_<cfg>.txt")
+    ap.add_argument("--measure-l2", action="store_true",
+                    help="run two rocprofv3 passes of L2 / TA / TD / TCP counters over --config "
+                         "and write profiles/l2_ta_<cfg>.txt")
     ap.add_argument("--measure-kernels", action="store_true",
                     help="run bench.py --config under rocprofv3 --kernel-trace --stats and "
                          "write profiles/fa_kernels_<cfg>_kernel_stats.txt")
@@ -861,6 +947,8 @@ def main() -> int:
         return _measure_traffic(args.config, out)
     if args.measure_sq:
         return _measure_sq(args.config, TRAFFIC_DIR / f"sq_counters_{args.config}.txt")
+    if args.measure_l2:
+        return _measure_l2(args.config, TRAFFIC_DIR / f"l2_ta_{args.config}.txt")
     if args.measure_kernels:
         return _measure_kernels(args.config,
                                 TRAFFIC_DIR / f"fa_kernels_{args.config}_kernel_stats.txt")
@@ -941,6 +1029,18 @@ def main() -> int:
                                      B, Hq, Hkv, T, D, dt_code, scale, launch_sp[0]))
         if ev is not None:
             ev[3].record(stream)
+
+    # Settle phase (untimed): an idle GPU starts a run below its loaded clocks, and a few
+    # warmup steps (under 1 ms of work at C2) do not bring it there.  Steps run in chunks
+    # of 8 until --settle-ms of wall time has passed; the warmup and the timed region
+    # below are unchanged by it.
+    settle_steps, t_settle = 0, time.perf_counter()
+    while args.settle_ms > 0 and (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for i in range(8):
+            launch(sets[(settle_steps + i) % nsets])
+        settle_steps += 8
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
 
     for i in range(args.warmup):
         launch(sets[i % nsets])
@@ -1114,6 +1214,10 @@ def main() -> int:
             "flop_per_launch": kern_flop,
         },
         "wall_s_timed": round(wall, 4),
+        "settle": {"steps": settle_steps, "seconds": round(settle_s, 3),
+                   "note": "untimed steps run before the warmup for at least --settle-ms of "
+                           "wall time (clocks at their loaded level); not part of the timed "
+                           "region"},
     }
     if gemm is not None:
         gemm["step_frac_of_gemm"] = round(step_tflops / gemm["tflops"], 4)

@@ -57,17 +57,17 @@ def test_fa_fwd_bwd(B, H, H_kv, T, D):
     assert_close_abs("lse", M, lse_ref, TOL_LSE)
 
 
-# ------------------------------------------------- the five workload configurations
+# ------------------------------------------------- the five workload configurations and the reference model's shape
 def _slices(cfg):
     """(b, kv-head) groups checked against the oracle (all of them when cheap)."""
-    if cfg.name in ("C1", "C2", "C3"):
+    if cfg.name in ("C1", "C2", "C3", "REF112M"):
         return None
     if cfg.name == "C4":
         return [(0, 0), (cfg.B - 1, cfg.Hkv - 1)]
     return [(cfg.B - 1, cfg.Hkv - 1)]
 
 
-@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5", "REF112M"])
 def test_config_parity(name):
     cfg = CONFIGS[name]
     announce(f"config {name} {cfg}")
@@ -112,12 +112,14 @@ def test_config_parity(name):
     (1, 32, 8, 4000),   # T > 3840: the forward's 256-row kernel too, T ragged
 ])
 def test_wide_d128_kernels(B, H, H_kv, T):
-    """Shapes with T > 1792 whose 256-row pairs fill the 256 resident workgroup slots of
-    an MI355X, so the dQ pass runs its 64-rows-per-wave kernel (and from T > 3840 the
-    forward too) (the smaller shapes above take the
-    128-row one); two (batch, kv-head) groups checked against the oracle."""
+    """Shapes with T > 1792 whose 256-row pairs number at least 256 (one per CU of an
+    MI355X), so the dQ pass runs its 64-rows-per-wave kernel (and from T > 3840 the
+    forward too) (the smaller shapes above take the 128-row one); the library's own
+    rule is asked which kernels run, and two (batch, kv-head) groups are checked against
+    the oracle."""
     D = 128
     announce(f"wide D=128 kernels B={B} H={H} Hkv={H_kv} T={T} D={D}")
+    assert _lib.d128_wide(B, H, T) == (T > 3840, True)
     q, k, v, do = make_custom(B, H, H_kv, T, D, torch.bfloat16, seed=3)
     o, M, dq, dk, dv = _run(q, k, v, do)
     G = H // H_kv

@@ -50,7 +50,7 @@ def test_oracle_reproduces_golden_outputs(name):
         assert max_abs(w, g[key]) < 1e-6, key  # stored as fp32
 
 
-@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5", "REF112M"])
 def test_workload_input_digests(name):
     ref = json.loads((GOLDEN / "input_digests.json").read_text())[name]
     q, k, v, do, ch = make_inputs(CONFIGS[name], seed=0)

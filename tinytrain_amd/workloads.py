@@ -54,6 +54,10 @@ CONFIGS: Dict[str, AttnConfig] = {
     "C3": AttnConfig("C3", 32, 12, 4, 1024, 64, torch.bfloat16, "qk", 1e-2),
     "C4": AttnConfig("C4", 4, 16, 8, 4096, 128, torch.bfloat16, "qk", 1e-2, outlier_frac=0.01),
     "C5": AttnConfig("C5", 1, 16, 8, 16384, 128, torch.bfloat16, "qk", 1e-2),
+    # The reference model's own attention shape (model.py:11-18: 8 query heads, 2 KV heads,
+    # head_dim 128, max_seq_len 512) at the batch its attn_impl comparison is quoted on
+    # (docs/results.md:184, B=32); inputs drawn like C2.
+    "REF112M": AttnConfig("REF112M", 32, 8, 2, 512, 128, torch.bfloat16, "qk", 1e-2),
 }
 
 def unit_rms(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
