@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define TTFA_ABI_VERSION 5
+#define TTFA_ABI_VERSION 6
 
 enum ttfa_dtype { TTFA_BF16 = 0, TTFA_F32 = 1 };
 
@@ -59,6 +59,17 @@ int ttfa_abi_version(void);
 /* Static description of a status code (negative: validation, positive: hipError_t).
  * No reference counterpart. */
 const char *ttfa_strerror(int code);
+
+/*
+ * Which bf16 D = 128 kernels ttfa_fwd / ttfa_bwd run for a shape: *fwd_wide and
+ * *dq_wide are set to 1 when the forward / the dQ pass use the 256-row kernels (64
+ * query rows per wave), 0 when they use the 128-row ones.  The two differ by
+ * rounding, and the choice is a rule on (B, Hq, T) alone, so a shape gives the same
+ * bits on every device.  Makes no HIP call.  TTFA_E_SEQ for B, Hq or T < 1,
+ * TTFA_E_NULL for a NULL output.  An introspection query for tests and profiling; no
+ * reference counterpart.
+ */
+int ttfa_d128_wide(int B, int Hq, int T, int *fwd_wide, int *dq_wide);
 
 /*
  * Forward: o = softmax(q k^T * scale, causal) v and lse, for every (b, hq).

@@ -45,6 +45,29 @@ def test_library_exports_every_declared_symbol():
 
 
 @needs_lib
+@needs_lib
+def test_d128_kernel_choice_is_a_rule_on_the_shape():
+    # The 256-row D = 128 kernels run where their pairs number at least 256 and T is long
+    # enough (dQ pass: T > 1792, forward: T > 3840); no HIP call, so it runs here.
+    cases = {
+        (4, 16, 4096): (True, True),      # C4
+        (1, 16, 16384): (True, True),     # C5
+        (32, 8, 512): (False, False),     # REF112M, the reference model's shape
+        (1, 64, 2000): (False, True),     # 64 heads x 4 pairs = 256: exactly one per CU
+        (1, 64, 1792): (False, False),    # 7 row tiles of 256: below the dQ threshold
+        (1, 63, 2000): (False, False),    # 252 pairs: fewer than 256
+        (1, 32, 4000): (True, True),      # 32 x 8 pairs
+        (1, 31, 4000): (False, False),    # 31 x 8 = 248 pairs
+    }
+    for (B, Hq, T), want in cases.items():
+        assert _lib.d128_wide(B, Hq, T) == want, (B, Hq, T)
+    lib = _lib.load()
+    f, d = ctypes.c_int(), ctypes.c_int()
+    assert lib.ttfa_d128_wide(0, 8, 512, ctypes.byref(f), ctypes.byref(d)) == _lib.E_SEQ
+    assert lib.ttfa_d128_wide(1, 8, 0, ctypes.byref(f), ctypes.byref(d)) == _lib.E_SEQ
+    assert lib.ttfa_d128_wide(1, 8, 512, None, ctypes.byref(d)) == _lib.E_NULL
+
+
 @pytest.mark.parametrize("code", [-1, -2, -3, -4, -5, -6, -7, -8, -9])
 def test_strerror_names_validation_codes(code):
     msg = _lib.strerror(code)

@@ -1,6 +1,5 @@
 """The generated stage schedules of the backward passes (tinytrain_amd/csrc/
-dkdv64_item.inc and dkdv128_item.inc for the dK/dV pass at D = 64 and 128, dq64_stage.inc
-for the D = 64 dQ pass).
+dkdv64_item.inc and dkdv128_item.inc for the dK/dV pass at D = 64 and 128).
 
 The generator inserts the LDS waits and hazard padding that the compiler does not add
 inside an asm statement.  This test re-checks the emitted text with an independent
@@ -168,29 +167,6 @@ def test_checker_catches_a_dropped_wait_or_nop():
         i = next(k for k, ln in enumerate(lines) if ln.startswith(prefix) and k > 2)
         with pytest.raises(AssertionError):
             _check_stream(lines[:i] + lines[i + 1:])
-
-
-def test_dq_committed_file_is_the_generator_output():
-    gen = _gen("gen_dq64_asm")
-    assert (CSRC / "dq64_stage.inc").read_text() == gen.render(), \
-        "dq64_stage.inc is stale: run python tinytrain_amd/csrc/gen_dq64_asm.py"
-
-
-@pytest.mark.parametrize("name", ["FULL", "DIAG0", "DIAG1", "DIAG2", "DIAG3", "RAGGED"])
-def test_dq_stream_rules_and_counts(name):
-    var = _variants(_gen("gen_dq64_asm").render(), "TTFA_DQ64_STAGE_ASM", "dq")
-    assert set(var) == {"FULL", "DIAG0", "DIAG1", "DIAG2", "DIAG3", "RAGGED"}
-    lines = var[name]
-    _check_stream(lines)
-    n_blocks = int(name[-1]) + 1 if name.startswith("DIAG") else 4
-    count = lambda p: sum(1 for ln in lines if ln.startswith(p))
-    assert count("v_mfma") == 12 * n_blocks           # S^T, dP^T: 8; dQ^T: 4 per block
-    assert count("ds_read") == 16 * n_blocks          # 8 row fragments, 8 transposed halves
-    assert count("v_exp_f32") == 16 * n_blocks
-    assert count("v_mov_b32") == 16 * n_blocks        # dP^T starts at -Delta
-    masked = {"FULL": 0, "RAGGED": 4}.get(name, 1)
-    assert count("v_cmp_gt_i32") == 16 * masked
-    assert count("v_cvt_pk_bf16_f32") == 8 * n_blocks
 
 
 # ---- D = 128 dK/dV stage (dkdv128_item.inc) -------------------------------------------

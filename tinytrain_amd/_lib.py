@@ -15,7 +15,7 @@ LIB_PATH = _PKG / "libttfa.so"
 
 TTFA_BF16 = 0
 TTFA_F32 = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Negative status codes of include/ttfa.h.
 E_NULL, E_HEAD_DIM, E_GROUP, E_SEQ, E_ALIGN, E_DTYPE, E_SCALE, E_EPS, E_QROWS, E_SCRATCH = (
@@ -24,7 +24,8 @@ BWD_STATIC_MAX_ROWS = 1 << 20  # TTFA_BWD_STATIC_MAX_ROWS
 EXPORTED = ("ttfa_abi_version", "ttfa_strerror", "ttfa_fwd", "ttfa_bwd", "ttfa_bwd_dq",
             "ttfa_bwd_dkdv", "ttfa_varlen_fwd", "ttfa_varlen_bwd", "ttfa_decode_workspace_bytes",
             "ttfa_decode_fwd", "ttfa_qk_prologue_fwd",
-            "ttfa_qk_prologue_workspace_bytes", "ttfa_qk_prologue_bwd", "ttfa_bwd_static")
+            "ttfa_qk_prologue_workspace_bytes", "ttfa_qk_prologue_bwd", "ttfa_bwd_static",
+            "ttfa_d128_wide")
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -58,7 +59,15 @@ _SIGS = {
     "ttfa_qk_prologue_workspace_bytes": ([_i] * 5, ctypes.c_longlong),
     "ttfa_qk_prologue_bwd": ([_vp] * 17 + [_i] * 5 + [_vp], _i),
     "ttfa_bwd_static": ([_vp] * 9 + [_i] * 6 + [_f, _vp], _i),
+    "ttfa_d128_wide": ([_i] * 3 + [ctypes.POINTER(_i)] * 2, _i),
 }
+
+
+def d128_wide(B: int, Hq: int, T: int) -> tuple[bool, bool]:
+    """(forward, dQ pass) of a bf16 D = 128 shape run the 256-row kernels (no HIP call)."""
+    f, d = _i(), _i()
+    check(load().ttfa_d128_wide(B, Hq, T, ctypes.byref(f), ctypes.byref(d)))
+    return bool(f.value), bool(d.value)
 
 
 def load() -> ctypes.CDLL:

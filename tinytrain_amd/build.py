@@ -56,15 +56,14 @@ def _compile(src: Path, extra: list[str]) -> Path:
 
 def _generate() -> None:
     """Rewrites generated sources whose generator output has changed: the D = 64 stage
-    schedules of the dK/dV pass (csrc/gen_dkdv64_asm.py -> csrc/dkdv64_item.inc) and of
-    the dQ pass (csrc/gen_dq64_asm.py -> csrc/dq64_stage.inc), and the D = 128 stage
-    schedule of the dK/dV pass (csrc/gen_dkdv128_asm.py -> csrc/dkdv128_item.inc) and of
+    schedule of the dK/dV pass (csrc/gen_dkdv64_asm.py -> csrc/dkdv64_item.inc), and the
+    D = 128 stage schedule of the dK/dV pass (csrc/gen_dkdv128_asm.py -> csrc/dkdv128_item.inc) and of
     the dQ pass (csrc/gen_dq128_asm.py -> csrc/dq128_stage.inc), and of the D = 128 forward
     (csrc/gen_fwd128_asm.py -> csrc/fwd128_stage.inc)."""
     import importlib
     sys.path.insert(0, str(CSRC))
     try:
-        gens = [importlib.import_module(m) for m in ("gen_dkdv64_asm", "gen_dq64_asm", "gen_dkdv128_asm",
+        gens = [importlib.import_module(m) for m in ("gen_dkdv64_asm", "gen_dkdv128_asm",
                                                          "gen_dq128_asm", "gen_fwd128_asm")]
     finally:
         sys.path.pop(0)

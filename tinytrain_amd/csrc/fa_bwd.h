@@ -1,8 +1,8 @@
 // Declarations shared by the backward translation units: the dK/dV pass's per-head view,
-// the kernel templates (fa_bwd.hip defines them; the D = 64 specializations of the batched
-// kernels are the hand-scheduled passes in fa_bwd_dq64.hip and fa_bwd_dkdv64.hip, while
-// packed variable-length sequences at D = 64 keep the generic bodies), the staged-tile
-// helpers of those passes and the dynamic-LDS opt-in.
+// the kernel templates (fa_bwd.hip defines them; the D = 64 and D = 128 specializations of
+// the batched dK/dV kernel are the hand-scheduled passes in fa_bwd_dkdv64.hip and
+// fa_bwd_dkdv128.hip, while packed variable-length sequences keep the generic bodies), the
+// staged-tile helpers of those passes and the dynamic-LDS opt-in.
 #pragma once
 
 #include <atomic>
@@ -35,13 +35,6 @@ __global__ void fa_bwd_dq_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__
                                       float *__restrict__ Delta, bf16 *__restrict__ dQ, int B,
                                       int Hq, int Hkv, int T, float scale_log2, float scale,
                                       int paired);
-template <>
-__global__ void fa_bwd_dq_bf16_kernel<64>(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
-                                          const bf16 *__restrict__ V, const bf16 *__restrict__ O,
-                                          const bf16 *__restrict__ dO,
-                                          const float *__restrict__ LSE, float *__restrict__ Delta,
-                                          bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
-                                          float scale_log2, float scale, int paired);
 // D = 128 dQ pass over 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): for launches
 // whose 256-row pairs fill the resident workgroup slots and whose T exceeds 1792.
 __global__ void fa_bwd_dq_wide_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,
@@ -78,10 +71,9 @@ __global__ void fa_bwd_dkdv_bf16_kernel<128>(const bf16 *__restrict__ Q, const b
                                              bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
                                              float scale_log2, float scale, int paired);
 // LDS bytes of the batched dK/dV passes: two 128-row stages of Q and dO tiles plus their
-// -LSE/scale and -Delta rows; of the D = 64 dQ pass: two 128-key stages of K and V tiles.
+// -LSE/scale and -Delta rows.
 constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
 constexpr int kDkv128LdsBytes = 2 * (2 * 128 * 128 * 2 + 2 * 128 * 4);
-constexpr int kDq64LdsBytes = 2 * 2 * 128 * 64 * 2;
 // D = 128 dQ pass: two 128-key stages of K and V tiles (workgroups of 256 query rows).
 constexpr int kDq128LdsBytes = 2 * 2 * 128 * 128 * 2;
 

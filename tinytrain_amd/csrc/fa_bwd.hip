@@ -301,9 +301,14 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
     }
   };
 
-  // The first K/V tile is in flight while this wave's rows load and Delta is formed:
-  // both wait on one memory round trip.
-  load_tile(0, 0);
+  // Key tiles run from the diagonal down to key 0.  The row tiles of one head that run
+  // at the same time (longest first) then read each K/V tile within a few tiles' time of
+  // each other, and a later, shorter row tile of the head starts on tiles the longer
+  // ones read recently, so K/V mostly come from L2 (in key order it would restart at
+  // key 0, read long before).  The first tile is in flight while this wave's rows load
+  // and Delta is formed: both wait on one memory round trip.
+  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
+  load_tile(n_kv - 1, 0);
   bf16x8 qf[KK], dof[KK];
   float dpart = 0.f;
 #pragma unroll
@@ -328,7 +333,6 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no register load is pending in the loop
   __syncthreads();
 
-  const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
   const int n_full = min((q0 + 1) / BN, T / BN);
   const int n_vis = min(n_kv, (q0 + 31) / BN + 1);
 
@@ -338,9 +342,10 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
 
   // No issue-priority steering here (the forward uses it): measured, it slowed both
   // backward passes.
-  for (int j = 0; j < n_kv; ++j) {
-    if (j + 1 < n_kv) load_tile(j + 1, (j + 1) & 1);
-    const bf16 *Kt = lds + (j & 1) * 2 * BN * D, *Vt = Kt + BN * D;
+  for (int jj = 0; jj < n_kv; ++jj) {
+    const int j = n_kv - 1 - jj;
+    if (j > 0) load_tile(j - 1, (jj + 1) & 1);
+    const bf16 *Kt = lds + (jj & 1) * 2 * BN * D, *Vt = Kt + BN * D;
     if (j < n_full)
       dq_tile<D, false>(Kt, Vt, qf, dof, ndelta, dqacc, lse_t, scale_log2, j * BN, qrow, T, lane);
     else if (j < n_vis)
@@ -583,20 +588,25 @@ __global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf1
   dkdv_rows<D>(smem, hd, kt, scale_log2, scale);
 }
 
+// 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): half the LDS and L2 bytes per
+// product, but half the workgroups and a longer prologue per workgroup, so only where its
+// pairs fill the 256 resident slots of an MI355X and carry at least 18 key stages each
+// (T > 1792; measured slower at T = 512 and 1024, faster from T = 2000 up).
+bool dq128_uses_wide(int B, int Hq, int T) {
+  const int n_wide = (T + 255) / 256;
+  return n_wide >= 8 && (int64_t)sched_items(true, n_wide, B, Hq) >= kWideSlots;
+}
+
 template <int D>
 static hipError_t launch_dq(const void *q, const void *k, const void *v, const void *o,
                             const void *dout, const float *lse, float *delta, void *dq, int B,
                             int Hq, int Hkv, int T, float scale, hipStream_t stream) {
   if constexpr (D == 128) {
-    // 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): half the LDS and L2 bytes per
-    // product, but half the workgroups and a longer prologue per workgroup, so only where
-    // its pairs fill the resident slots and carry at least 18 key stages each (T > 1792;
-    // measured slower at T = 512 and 1024, faster from T = 2000 up).
-    const int n_wide = (T + 255) / 256;
-    hipError_t e = allow_lds<fa_bwd_dq_wide_bf16_kernel>(kDq128LdsBytes);  // before the
-    if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
-    const int slots = resident_slots<fa_bwd_dq_wide_bf16_kernel>(256, kDq128LdsBytes);
-    if (n_wide >= 8 && sched_items(true, n_wide, B, Hq) >= slots) {
+    if (dq128_uses_wide(B, Hq, T)) {
+      const int n_wide = (T + 255) / 256;
+      hipError_t e = allow_lds<fa_bwd_dq_wide_bf16_kernel>(kDq128LdsBytes);  // before the
+      if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
+      const int slots = resident_slots<fa_bwd_dq_wide_bf16_kernel>(256, kDq128LdsBytes);
       const bool paired = use_pairs(n_wide, B, Hq, slots);
       const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
       fa_bwd_dq_wide_bf16_kernel<<<grid, block, kDq128LdsBytes, stream>>>(
@@ -606,7 +616,7 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
     }
   }
   const int n_tiles = (T + DqTile<D>::BM - 1) / DqTile<D>::BM;
-  constexpr size_t lds = D == 64 ? kDq64LdsBytes : DqTile<D>::LDS_BYTES;
+  constexpr size_t lds = DqTile<D>::LDS_BYTES;
   auto kern = fa_bwd_dq_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds<fa_bwd_dq_bf16_kernel<D>>(lds);

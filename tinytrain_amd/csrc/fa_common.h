@@ -236,8 +236,9 @@ __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 // Workgroup -> work item.  Causal row tiles carry very different amounts of work (tile t
 // of n sees t+1 key tiles), so every workgroup takes a PAIR of row tiles (n-1-p, p):
 // the pair's total work is the same for every p, and a grid of pairs is one balanced
-// round instead of a long tail behind the diagonal's longest tiles.  The longer tile of
-// the pair runs first.  When n is odd the middle tile forms a pair of its own.
+// round instead of a long tail behind the diagonal's longest tiles.  `first` is the
+// longer tile of the pair; each kernel chooses which of the two it runs first.  When n
+// is odd the middle tile forms a pair of its own.
 //
 // Hardware hands consecutive workgroup ids to the 8 XCDs round-robin (id % 8), and each
 // XCD has its own L2.  (This holds for a whole MI355X, SPX mode.  The grouping below is
@@ -320,7 +321,8 @@ inline int sched_items(bool paired, int n_tiles, int B, int H) {
 // Workgroups of kernel KERN resident on the current device at once: CUs x blocks per CU,
 // from the runtime's occupancy calculator, cached per kernel and device (devices 0..63;
 // a higher id is asked every time).  The value only picks the work schedule (pairs or
-// single row tiles), never the results.
+// single row tiles), never the results: which kernel a shape runs is a rule on the shape
+// alone (fwd128_uses_wide, dq128_uses_wide).
 template <auto KERN>
 inline int resident_slots(int block, size_t lds) {
   static std::atomic<int> cached[64];

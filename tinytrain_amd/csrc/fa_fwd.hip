@@ -261,8 +261,16 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_bf16_kernel(
   const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D;
   const FwdHead hd{Q + w.bh * hs, K + kvh * hs, V + kvh * hs, O + w.bh * hs,
                    LSE + (int64_t)w.bh * T, T};
-  fwd_rows<D>(lds, hd, w.first, scale_log2, w1 + w2, wmax);
-  if (w.second >= 0) fwd_rows<D>(lds, hd, w.second, scale_log2, w2, wmax);
+  // A pair runs its shorter tile first.  The workgroups of one head start together and
+  // read key tiles 0, 1, ... of the same K/V, and each then re-reads them in its longer
+  // tile within a few tiles of the previous read, so K/V come from L2 (long tile first,
+  // the short tile re-read keys from the launch's start, by then evicted).
+  if (w.second >= 0) {
+    fwd_rows<D>(lds, hd, w.second, scale_log2, w1 + w2, wmax);
+    fwd_rows<D>(lds, hd, w.first, scale_log2, w1, wmax);
+  } else {
+    fwd_rows<D>(lds, hd, w.first, scale_log2, w1, wmax);
+  }
 }
 
 // Packed variable-length sequences ([H, total, D] per tensor, sequence s at rows
@@ -305,28 +313,31 @@ __global__ void fa_fwd_wide_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *
                                         float scale_log2, int paired);
 constexpr int kFwd128LdsBytes = 2 * 2 * 128 * 128 * 2;  // two 128-key stages of K and V
 
+// 256-row tiles, 64 rows per wave: half the LDS bytes per product, but half the
+// workgroups and a longer prologue, so only where its pairs fill the 256 resident slots of
+// an MI355X and T > 3840 (measured 5-7% slower at T = 2000-3072, even at 4096, 3-5% faster
+// from 8192 up).
+bool fwd128_uses_wide(int B, int Hq, int T) {
+  const int n_wide = (T + 255) / 256;
+  return n_wide >= 16 && (int64_t)sched_items(true, n_wide, B, Hq) >= kWideSlots;
+}
+
 hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
                            int B, int Hq, int Hkv, int T, int D, float scale,
                            hipStream_t stream) {
   const int n_tiles = (T + FwdTile<64>::BM - 1) / FwdTile<64>::BM;
   const float sl2 = scale * kLog2e;
-  if (D == 128) {
-    // 256-row tiles, 64 rows per wave: half the LDS bytes per product, but half the
-    // workgroups and a longer prologue, so only where its pairs fill the resident slots
-    // and T > 3840 (measured 5-7% slower at T = 2000-3072, even at 4096, 3-5% faster
-    // from 8192 up)
+  if (D == 128 && fwd128_uses_wide(B, Hq, T)) {
     const int n_wide = (T + 255) / 256;
     hipError_t e = allow_lds<fa_fwd_wide_bf16_kernel>(kFwd128LdsBytes);  // before the
     if (e != hipSuccess) return e;  // occupancy query, which sees the raised limit
     const int slots = resident_slots<fa_fwd_wide_bf16_kernel>(256, kFwd128LdsBytes);
-    if (n_wide >= 16 && sched_items(true, n_wide, B, Hq) >= slots) {
-      const bool paired = use_pairs(n_wide, B, Hq, slots);
-      const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
-      fa_fwd_wide_bf16_kernel<<<grid, block, kFwd128LdsBytes, stream>>>(
-          (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o, lse, B, Hq, Hkv, T, sl2,
-          (int)paired);
-      return hipGetLastError();
-    }
+    const bool paired = use_pairs(n_wide, B, Hq, slots);
+    const dim3 grid((unsigned)sched_items(paired, n_wide, B, Hq)), block(256);
+    fa_fwd_wide_bf16_kernel<<<grid, block, kFwd128LdsBytes, stream>>>(
+        (const bf16 *)q, (const bf16 *)k, (const bf16 *)v, (bf16 *)o, lse, B, Hq, Hkv, T, sl2,
+        (int)paired);
+    return hipGetLastError();
   }
   auto go = [&](auto kern, int slots) {
     const bool paired = use_pairs(n_tiles, B, Hq, slots);

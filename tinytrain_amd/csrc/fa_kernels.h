@@ -8,6 +8,14 @@ namespace ttfa {
 
 hipError_t launch_fwd_bf16(const void *q, const void *k, const void *v, void *o, float *lse,
                            int B, int Hq, int Hkv, int T, int D, float scale, hipStream_t stream);
+
+// Which bf16 D = 128 kernels a shape runs: the 256-row forward / dQ pass (64 rows per wave)
+// or the 128-row ones.  A fixed rule on the shape alone (never on the device's occupancy),
+// so a shape's output bits are the same on every device: the wide kernels differ from the
+// 128-row ones by rounding.
+constexpr int kWideSlots = 256;  // one 256-row workgroup per CU on the 256 CUs of an MI355X
+bool fwd128_uses_wide(int B, int Hq, int T);
+bool dq128_uses_wide(int B, int Hq, int T);
 hipError_t launch_bwd_dq_bf16(const void *q, const void *k, const void *v, const void *o,
                               const void *dout, const float *lse, float *delta, void *dq,
                               int B, int Hq, int Hkv, int T, int D, float scale,

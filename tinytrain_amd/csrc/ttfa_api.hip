@@ -102,6 +102,14 @@ extern "C" {
 
 int ttfa_abi_version(void) { return TTFA_ABI_VERSION; }
 
+int ttfa_d128_wide(int B, int Hq, int T, int *fwd_wide, int *dq_wide) {
+  if (!fwd_wide || !dq_wide) return TTFA_E_NULL;
+  if (B < 1 || Hq < 1 || T < 1) return TTFA_E_SEQ;
+  *fwd_wide = ttfa::fwd128_uses_wide(B, Hq, T) ? 1 : 0;
+  *dq_wide = ttfa::dq128_uses_wide(B, Hq, T) ? 1 : 0;
+  return TTFA_OK;
+}
+
 const char *ttfa_strerror(int code) {
   switch (code) {
     case TTFA_OK: return "success";
