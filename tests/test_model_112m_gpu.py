@@ -23,11 +23,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 # hip's deviation from the fp32 logits, as a multiple of sdpa-bf16's own deviation.  The
 # mean is the tight bound: it measured 0.996-1.002 on every box.  The maximum is set by a
-# handful of logits; the compiled model around the (deterministic) attention kernels gives
-# different bf16 results on different boxes, and the ratio of the maxima measured
-# 0.97-1.02 on one box and 1.16 on another for the same code, so its bound leaves room
-# for that spread.  A wrong mask, scale or head map moves both far beyond these bounds.
-MAX_RATIO = 1.5
+# handful of logits.  Eager, every kernel is deterministic and the ratio of the maxima is
+# bounded as tightly as the mean's spread allows.  Compiled, the generated kernels around
+# the attention ops round differently from box to box: the ratio of the maxima read
+# 0.97-1.02 on one box and 1.16 on another for the same code (the per-box values are
+# kept in profiles/model_112m_logits.txt), so that bound leaves room for the spread.  A
+# wrong mask, scale or head map moves both far beyond these bounds.
+MAX_RATIO_EAGER = 1.15
+MAX_RATIO_COMPILED = 1.5
 MEAN_RATIO = 1.05
 
 
@@ -58,13 +61,15 @@ def _logits(model, x, impl, fused=False, compiled=False):
     return out
 
 
-def _check(name, got, sdpa, ref):
+def _check(name, got, sdpa, ref, max_ratio):
     e_hip, e_sdpa = (got - ref).abs(), (sdpa - ref).abs()
     msg = (f"{name}: |hip - fp32| max {e_hip.max().item():.5f} mean {e_hip.mean().item():.6f}; "
-           f"|sdpa_bf16 - fp32| max {e_sdpa.max().item():.5f} mean {e_sdpa.mean().item():.6f}")
+           f"|sdpa_bf16 - fp32| max {e_sdpa.max().item():.5f} mean {e_sdpa.mean().item():.6f}; "
+           f"ratios max {(e_hip.max() / e_sdpa.max()).item():.4f} "
+           f"mean {(e_hip.mean() / e_sdpa.mean()).item():.4f}")
     print(msg, flush=True)
     assert torch.isfinite(got).all(), msg
-    assert e_hip.max() <= MAX_RATIO * e_sdpa.max(), msg
+    assert e_hip.max() <= max_ratio * e_sdpa.max(), msg
     assert e_hip.mean() <= MEAN_RATIO * e_sdpa.mean(), msg
 
 
@@ -72,12 +77,14 @@ def test_112m_logits_eager(model_112m):
     announce("112M logits eager: hip, hip + fused prologue vs sdpa bf16 vs fp32")
     model, x, ref = model_112m
     sdpa = _logits(model, x, "sdpa")
-    _check("hip eager", _logits(model, x, "hip"), sdpa, ref)
-    _check("hip + fused prologue eager", _logits(model, x, "hip", fused=True), sdpa, ref)
+    _check("hip eager", _logits(model, x, "hip"), sdpa, ref, MAX_RATIO_EAGER)
+    _check("hip + fused prologue eager", _logits(model, x, "hip", fused=True), sdpa, ref,
+           MAX_RATIO_EAGER)
 
 
 def test_112m_logits_compiled(model_112m):
     announce("112M logits torch.compile: hip vs sdpa bf16 vs fp32")
     model, x, ref = model_112m
     sdpa = _logits(model, x, "sdpa", compiled=True)
-    _check("hip compiled", _logits(model, x, "hip", compiled=True), sdpa, ref)
+    _check("hip compiled", _logits(model, x, "hip", compiled=True), sdpa, ref,
+           MAX_RATIO_COMPILED)
