@@ -8,6 +8,13 @@
 // a stage is one hand-scheduled instruction stream (gen_dq128_asm.py) in which every K/V
 // fragment read from LDS feeds the products of both row groups: half the LDS bytes per
 // product of a 32-row wave, whose LDS delivery bounds that form of the pass.
+//
+// The AGPR state lives outside every asm operand list, so it is only correct while the
+// compiler itself touches no AGPR in this kernel.  Guards that must stay in the test
+// suite: tests/test_asm_contracts.py (compiled code: no AGPR access outside the inline
+// asm, no spills, no VALU write of an inline MFMA's source within two wait states) and
+// the parity tests that select this kernel (test_wide_d128_kernels, which also asserts
+// the kernel choice through ttfa_d128_wide, and test_config_parity[C4] / [C5]).
 #include "dq128_stage.inc"
 #include "fa_bwd.h"
 #include "fa_common.h"

@@ -6,6 +6,13 @@
 // wave's work on a stage is one hand-scheduled instruction stream (gen_fwd128_asm.py) in
 // which every K row and V^T fragment read from LDS feeds the products of both row groups:
 // half the LDS bytes per product of the 32-row kernel (fa_fwd.hip).
+//
+// The AGPR state lives outside every asm operand list, so it is only correct while the
+// compiler itself touches no AGPR in this kernel.  Guards that must stay in the test
+// suite: tests/test_asm_contracts.py (compiled code: no AGPR access outside the inline
+// asm, no spills, no VALU write of an inline MFMA's source within two wait states) and
+// the parity tests that select this kernel (test_wide_d128_kernels, which also asserts
+// the kernel choice through ttfa_d128_wide, and test_config_parity[C4] / [C5]).
 #include "fa_bwd.h"  // lds_addr
 #include "fa_common.h"
 #include "fwd128_stage.inc"
