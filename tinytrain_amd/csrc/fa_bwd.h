@@ -1,8 +1,8 @@
 // Declarations shared by the backward translation units: the dK/dV pass's per-head view,
-// the kernel templates (fa_bwd.hip defines them; the D = 64 and D = 128 specializations of
-// the batched dK/dV kernel are the hand-scheduled passes in fa_bwd_dkdv64.hip and
-// fa_bwd_dkdv128.hip, while packed variable-length sequences keep the generic bodies), the
-// staged-tile helpers of those passes and the dynamic-LDS opt-in.
+// the kernel templates (fa_bwd.hip defines the dQ kernels; the dK/dV kernels, batched and
+// packed variable-length, exist only as the D = 64 and D = 128 specializations in
+// fa_bwd_dkdv64.hip and fa_bwd_dkdv128.hip, hand-scheduled stage streams), the staged-tile
+// helpers of those passes and the dynamic-LDS opt-in.
 #pragma once
 
 #include <atomic>
@@ -70,8 +70,20 @@ __global__ void fa_bwd_dkdv_bf16_kernel<128>(const bf16 *__restrict__ Q, const b
                                              const float *__restrict__ Delta, bf16 *__restrict__ dK,
                                              bf16 *__restrict__ dV, int B, int Hq, int Hkv, int T,
                                              float scale_log2, float scale, int paired);
-// LDS bytes of the batched dK/dV passes: two 128-row stages of Q and dO tiles plus their
-// -LSE/scale and -Delta rows.
+template <>
+__global__ void fa_bwd_dkdv_varlen_bf16_kernel<64>(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE, const float *__restrict__ Delta,
+    bf16 *__restrict__ dK, bf16 *__restrict__ dV, const int *__restrict__ cu_seqlens, int n_seq,
+    int total, int max_seqlen, int Hq, int Hkv, float scale_log2, float scale);
+template <>
+__global__ void fa_bwd_dkdv_varlen_bf16_kernel<128>(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE, const float *__restrict__ Delta,
+    bf16 *__restrict__ dK, bf16 *__restrict__ dV, const int *__restrict__ cu_seqlens, int n_seq,
+    int total, int max_seqlen, int Hq, int Hkv, float scale_log2, float scale);
+// LDS bytes of the dK/dV passes (batched and packed varlen): two 128-row stages of Q and dO
+// tiles plus their -LSE/scale and -Delta rows.
 constexpr int kDkv64LdsBytes = 2 * (2 * 128 * 64 * 2 + 2 * 128 * 4);
 constexpr int kDkv128LdsBytes = 2 * (2 * 128 * 128 * 2 + 2 * 128 * 4);
 // D = 128 dQ pass: two 128-key stages of K and V tiles (workgroups of 256 query rows).

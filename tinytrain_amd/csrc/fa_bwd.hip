@@ -8,7 +8,8 @@
 //     a workgroup takes a balanced pair of row tiles, the longer first (pair_item), when
 //     pairs fill whole rounds of the resident slots; at D = 64 it takes one row tile,
 //     longest first, so the row body is inlined once and three workgroups per CU fit
-//     without spills.
+//     without spills.  Key tiles run from the row tile's diagonal down to key 0.  (Long
+//     sequences at D = 128 take the 256-row pass of fa_bwd_dq128.hip.)
 //     The prologue computes Delta = rowsum(O * dO) for the tile's own rows from the
 //     same registers that hold dO, and writes it to the workspace
 //     for pass 2 (so there is no separate preprocess launch and dO is read once here).
@@ -19,19 +20,13 @@
 //     dS^T = P^T (dP^T - Delta), dQ^T += K^T dS^T with K^T read by ds_read_b64_tr_b16.
 //     Every lane owns one query row, so LSE and Delta are per-lane scalars.
 //
-//  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159).  A key tile = 128 keys of one
-//     (batch, kv head), 4 waves x 32 keys; a workgroup takes a balanced pair of key
-//     tiles when pairs fill whole rounds of the resident slots, else one key tile,
-//     longest first.  The wave's K and V rows stay in registers.
-//     The workgroup walks the G query heads of its group and, for each, the 64-row Q
-//     tiles from the diagonal to the end, double-buffered through LDS together with the
-//     tiles' -LSE/scale and -Delta; dK and dV accumulate in registers across the whole
-//     group, so the group reduction needs no atomics and the result is bitwise
-//     deterministic (reference loop :125-152).  Per wave and 32-row block:
-//     S - LSE/scale = Q K^T - LSE/scale and dP - Delta = dO V^T - Delta (accumulators
-//     initialised from the staged rows),
-//     P, dS, then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
-//     from LDS.  dK is scaled once at the end (:154).
+//  2. dK/dV pass (reference: bwd_dkdv_kernel :93-159): fa_bwd_dkdv64.hip and
+//     fa_bwd_dkdv128.hip, whose per-stage work is a generated instruction stream; this
+//     file holds their launchers.  A key tile = 128 keys of one (batch, kv head), 4 waves
+//     x 32 keys, walking the G query heads of its group and their 128-row Q/dO stages from
+//     the diagonal to the end; dK and dV accumulate in registers across the whole group,
+//     so the group reduction needs no atomics and the result is bitwise deterministic
+//     (reference loop :125-152).
 //
 // Both passes fill their LDS tiles with buffer_load ... lds (global -> LDS, 16 bytes per
 // lane, no staging VGPRs), the next tile's loads in flight while the current tile is
@@ -45,11 +40,8 @@ namespace ttfa {
 
 namespace {
 
-// The K/V tiles of the dQ pass and the Q/dO tiles of the D=128 dK/dV pass use layout 1
-// (conflict-free row reads); the D=64 varlen dK/dV pass keeps swz<64>.
+// The K/V tiles of the dQ pass use layout 1 (conflict-free row reads).
 constexpr int kDqLayout = 1;
-template <int D>
-constexpr int kDkvLayout = D == 128 ? 1 : 0;
 
 template <int D>
 struct DqTile {
@@ -60,32 +52,6 @@ struct DqTile {
   static constexpr int LOADS = BN * CH / 256;    // 16-byte loads per thread per K (or V) tile
   static constexpr int LDS_BYTES = 2 * 2 * BN * D * 2;  // [stage][K|V] bf16
 };
-
-template <int D>
-struct DkvTile {
-  static constexpr int BNK = 128;                // keys per workgroup
-  static constexpr int BMQ = 64;                 // query rows per LDS tile
-  static constexpr int KK = D / 16, DB = D / 32, CH = D / 8;
-  static constexpr int LOADS = BMQ * CH / 256;   // 16-byte loads per thread per Q (or dO) tile
-  // [stage][Q|dO] bf16 tiles, then [stage][-LSE/scale | -Delta] fp32 rows
-  static constexpr int LDS_BYTES = 2 * 2 * BMQ * D * 2 + 2 * 2 * BMQ * 4;
-};
-
-// S/dP products of the D = 128 dK/dV pass with the accumulator in VGPRs and the K/V
-// operand in AGPRs.  That kernel needs AGPRs (dK/dV), so the builtin gets the AGPR form
-// for all its MFMAs and every S/dP result would cross back to VGPRs (v_accvgpr_read) for
-// the exponentials: 64 copies per item on SIMDs that hold one wave.  The compiler's
-// hazard checks do not see inside inline asm, so the operands must not come from a VALU
-// write just before (here: LDS reads, buffer loads, and the previous product of the
-// same chain), and a chain ends with mfma_vacc_drain before any VALU reads its result.
-__device__ __forceinline__ void mfma32_vacc(f32x16 &acc, bf16x8 a, bf16x8 b_agpr) {
-  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "a"(b_agpr));
-}
-// 24 wait states after a chain of mfma32_vacc, twice what the compiler puts between a
-// product of this shape and a VALU read of its result.
-__device__ __forceinline__ void mfma_vacc_drain(f32x16 &x, f32x16 &y) {
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(x), "+v"(y));
-}
 
 // One key tile of the dQ pass for one wave, one 32-key block at a time.
 template <int D, bool MASK>
@@ -147,94 +113,6 @@ __device__ __forceinline__ void dq_tile(const bf16 *Kt, const bf16 *Vt, const bf
       for (int db = 0; db < P::DB; ++db) kt[db] = lds_read_trT<D, kDqLayout>(Kt, 32 * kb + 16 * m, 32 * db, lane);
 #pragma unroll
       for (int db = 0; db < P::DB; ++db) dqacc[db] = mfma32(kt[db], dsb, dqacc[db]);
-    }
-  }
-}
-
-// NB consecutive 32-row query blocks (qb0..) of the dK/dV pass for one wave (its 32 keys).
-// Both accumulator chains of a block start from values staged in LDS in the S-result
-// layout (register 4a+e = row 8a+4lg+e): S from -LSE/scale and dP from -Delta, so
-// P = exp2(S' * scale*log2e) and dS = P (dP - Delta) each take one multiply.  With
-// NB = 2 the blocks' independent MFMA chains and exponentials interleave.
-template <int D, int NB, bool MASK>
-__device__ __forceinline__ void dkdv_blocks(const bf16 *Qt, const bf16 *dOt, const float *nls_t,
-                                            const float *nd_t, const bf16x8 (&kf)[D / 16],
-                                            const bf16x8 (&vf)[D / 16], f32x16 (&dkacc)[D / 32],
-                                            f32x16 (&dvacc)[D / 32], int qb0, int qbase0, int krow,
-                                            int T, float scale_log2, int lane) {
-  using P = DkvTile<D>;
-  const int lq = lane & 31, lg = lane >> 5;
-  f32x16 s[NB], dp[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int qb = qb0 + nb;
-    f32x16 ns, nd;
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const f32x4 x = *reinterpret_cast<const f32x4 *>(nls_t + qb * 32 + 8 * a + 4 * lg);
-      const f32x4 y = *reinterpret_cast<const f32x4 *>(nd_t + qb * 32 + 8 * a + 4 * lg);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ns[4 * a + e] = x[e];
-        nd[4 * a + e] = y[e];
-      }
-    }
-    bf16x8 qa[P::KK], da[P::KK];
-#pragma unroll
-    for (int kk = 0; kk < P::KK; ++kk) {
-      qa[kk] = lds_read_row8<D, kDkvLayout<D>>(Qt, qb * 32 + lq, 2 * kk + lg);
-      da[kk] = lds_read_row8<D, kDkvLayout<D>>(dOt, qb * 32 + lq, 2 * kk + lg);
-    }
-    if constexpr (D == 128) {
-      s[nb] = ns;
-      dp[nb] = nd;
-#pragma unroll
-      for (int kk = 0; kk < P::KK; ++kk) {
-        mfma32_vacc(s[nb], qa[kk], kf[kk]);
-        mfma32_vacc(dp[nb], da[kk], vf[kk]);
-      }
-      mfma_vacc_drain(s[nb], dp[nb]);
-    } else {
-      s[nb] = mfma32(qa[0], kf[0], ns);
-      dp[nb] = mfma32(da[0], vf[0], nd);
-#pragma unroll
-      for (int kk = 1; kk < P::KK; ++kk) {
-        s[nb] = mfma32(qa[kk], kf[kk], s[nb]);
-        dp[nb] = mfma32(da[kk], vf[kk], dp[nb]);
-      }
-    }
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float x = s[nb][r] * scale_log2;
-      if (MASK) {
-        const int qr = qbase0 + nb * 32 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (krow > qr || qr >= T) x = -INFINITY;
-      }
-      const float p = exp2f_fast(x);
-      s[nb][r] = p;
-      dp[nb][r] = p * dp[nb][r];  // dS
-    }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int qb = qb0 + nb;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const bf16x8 pb = pack8(s[nb], 8 * m);
-      const bf16x8 dsb = pack8(dp[nb], 8 * m);
-      bf16x8 dot[P::DB], qt[P::DB];
-#pragma unroll
-      for (int db = 0; db < P::DB; ++db) {
-        dot[db] = lds_read_trT<D, kDkvLayout<D>>(dOt, qb * 32 + 16 * m, 32 * db, lane);
-        qt[db] = lds_read_trT<D, kDkvLayout<D>>(Qt, qb * 32 + 16 * m, 32 * db, lane);
-      }
-#pragma unroll
-      for (int db = 0; db < P::DB; ++db) {
-        dvacc[db] = mfma32(dot[db], pb, dvacc[db]);
-        dkacc[db] = mfma32(qt[db], dsb, dkacc[db]);
-      }
     }
   }
 }
@@ -412,181 +290,9 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_varlen_bf16_
 }
 
 // ---------------------------------------------------------------- pass 2: dK, dV
-// (The batched kernel at D = 64 is the hand-scheduled pass in fa_bwd_dkdv64.hip; this
-// body serves D = 128 and the packed variable-length kernel at both head dims.)
-// dK and dV for the 128 keys of key tile kt of one KV head, reduced over the head's
-// query-head group.  Ends with a workgroup barrier, so the caller may reuse the LDS ring
-// right away.
-template <int D>
-__device__ __forceinline__ void dkdv_rows(bf16 *lds, const DkvHead &hd, int kt, float scale_log2,
-                                          float scale) {
-  using P = DkvTile<D>;
-  constexpr int BNK = P::BNK, BMQ = P::BMQ, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
-  float *const ldsf = reinterpret_cast<float *>(lds + 2 * 2 * BMQ * D);
-  const int G = hd.G, T = hd.T;
-
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int lq = lane & 31, lg = lane >> 5;
-  const int k0w = kt * BNK + wave * 32;  // first key of this wave
-  const int krow = k0w + lq;
-
-  const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const auto rk = make_rsrc(hd.k, head_bytes);
-  const auto rv = make_rsrc(hd.v, head_bytes);
-
-  // K^T, V^T as B operands: lane (key lq, lg) slot s of step kk = row krow, d = 16kk+8lg+s.
-  bf16x8 kf[KK], vf[KK];
-#pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    const uint32_t off = (uint32_t)(krow * D + 16 * kk + 8 * lg) * 2;
-    kf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rk, off));
-    vf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rv, off));
-  }
-  if constexpr (D == 128) {
-    // K/V fragments live in AGPRs at D = 128 (operands of the S/dP products there).
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) asm volatile("" : "+a"(kf[kk]), "+a"(vf[kk]));
-  }
-
-  const int n_qt = (T + BMQ - 1) / BMQ;
-  const int qt_lo = kt * (BNK / BMQ);
-  const int per_g = n_qt - qt_lo;
-  const int n_items = G * per_g;
-
-  const float inv_scale = 1.f / scale;
-  // Threads < 128 carry one LSE (tid < 64) or Delta value of the next item from its load
-  // to its staging: loaded raw, so nothing waits on the load (nor on the Q/dO tile loads
-  // issued before it) until the value is staged after the current item's compute.
-  float fl = 0.f;
-  const uint32_t row_bytes = (uint32_t)T * 4;  // LSE / Delta rows past T read as zero
-  // Items run over the group's query heads g, and for each over the query tiles
-  // qt_lo..n_qt-1; (ld_g, ld_qt) is the next item to load.
-  int ld_g = 0, ld_qt = qt_lo;
-  // The load addresses use a scalar copy of the wave index (LDS destinations in SGPRs);
-  // the compute keeps the vector one, which here gives the better register allocation.
-  const int wave_u = wave_id();
-  auto load_item = [&](int stage) {
-    bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-    const int g = ld_g, qt = ld_qt;
-    if (++ld_qt == n_qt) {
-      ld_qt = qt_lo;
-      ++ld_g;
-    }
-    const auto rq = make_rsrc(hd.q + g * hd.head_stride, head_bytes);
-    const auto rdo = make_rsrc(hd.dout + g * hd.head_stride, head_bytes);
-    const float *lse_g = hd.lse + g * hd.row_stride, *delta_g = hd.delta + g * hd.row_stride;
-    const auto rfl = make_rsrc(wave_u == 0 ? lse_g : delta_g, row_bytes);  // wave-uniform
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int e0 = 256 * i + 64 * wave_u, e = e0 + lane, row = e / CH, pc = e % CH;
-      const uint32_t off = (uint32_t)((qt * BMQ + row) * D + swz_l<D, kDkvLayout<D>>(row, pc) * 8) * 2;
-      buf_load16_lds(rq, off, Qt + e0 * 8);
-      buf_load16_lds(rdo, off, dOt + e0 * 8);
-    }
-    if (tid < 2 * BMQ)
-      fl = __uint_as_float(buf_load4(rfl, (uint32_t)(qt * BMQ + (tid & (BMQ - 1))) * 4));
-  };
-  auto stage_rows = [&](int stage) {
-    if (tid < 2 * BMQ) ldsf[stage * 2 * BMQ + tid] = tid < BMQ ? -fl * inv_scale : -fl;
-  };
-
-  f32x16 dkacc[DB], dvacc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    dkacc[db] = f32x16{};
-    dvacc[db] = f32x16{};
-  }
-
-  if (n_items > 0) {
-    load_item(0);
-    stage_rows(0);
-  }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K/V registers complete before the loop
-  __syncthreads();
-  int qt = qt_lo;  // query tile of the current item
-  for (int it = 0; it < n_items; ++it) {
-    if (it + 1 < n_items) load_item((it + 1) & 1);
-    const int stage = it & 1;
-    const bf16 *Qt = lds + stage * 2 * BMQ * D, *dOt = Qt + BMQ * D;
-    const float *nls_t = ldsf + stage * 2 * BMQ, *nd_t = nls_t + BMQ;
-    const int qbase = qt * BMQ;
-    if (++qt == n_qt) qt = qt_lo;
-    if (qbase >= k0w + 31 && qbase + BMQ - 1 < T) {
-      // every row of the tile sees every key of the wave: both blocks together, unmasked
-      dkdv_blocks<D, BMQ / 32, false>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, 0, qbase, krow,
-                                      T, scale_log2, lane);
-    } else {
-#pragma unroll
-      for (int qb = 0; qb < BMQ / 32; ++qb) {
-        const int qb_row = qbase + qb * 32;
-        if (qb_row + 31 < k0w) continue;  // every row of the block precedes every key
-        if (qb_row >= k0w + 31 && qb_row + 31 < T)
-          dkdv_blocks<D, 1, false>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, qb, qb_row, krow,
-                                   T, scale_log2, lane);
-        else
-          dkdv_blocks<D, 1, true>(Qt, dOt, nls_t, nd_t, kf, vf, dkacc, dvacc, qb, qb_row, krow,
-                                  T, scale_log2, lane);
-      }
-    }
-    if (it + 1 < n_items) stage_rows((it + 1) & 1);
-    wait_vm_all();  // item it+1's Q/dO tiles are in LDS before any wave passes the barrier
-    __syncthreads();
-  }
-
-  // The loop's last barrier freed the LDS ring: each wave stages its dK and dV tiles in
-  // its own two 32*D slices of it for row-contiguous stores.
-  store_rows<D>(dkacc, scale, lds + wave * 64 * D, hd.dk, k0w, T, lane);
-  store_rows<D>(dvacc, 1.f, lds + wave * 64 * D + 32 * D, hd.dv, k0w, T, lane);
-  __syncthreads();  // the ring is free again for the caller
-}
-
-template <int D>
-__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_bf16_kernel(
-    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
-    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV, int B,
-    int Hq, int Hkv, int T, float scale_log2, float scale, int paired) {
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  using P = DkvTile<D>;
-  const int n_ktiles = (T + P::BNK - 1) / P::BNK;
-  // Key tile 0 sees the most query rows, so the longer tile of a pair is the low one.
-  const WorkPair w = sched_item(paired, blockIdx.x, n_ktiles, B, Hkv, 1, true);
-  const int G = Hq / Hkv;
-  const int b = w.bh / Hkv, hk = w.bh - b * Hkv;
-  const int64_t hs = (int64_t)T * D, kvb = w.bh * hs, q0 = (int64_t)b * Hq + hk * G;
-  const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs, dO + q0 * hs,
-                   LSE + q0 * T, Delta + q0 * T, hs, T, G, T};
-  dkdv_rows<D>(smem, hd, w.first, scale_log2, scale);
-  if (w.second >= 0) dkdv_rows<D>(smem, hd, w.second, scale_log2, scale);
-}
-
-// Packed variable-length sequences (layouts as for the varlen dQ pass).  Workgroup ->
-// (key tile rank, sequence, KV head), rank-major; key tile 0 of a sequence sees the most
-// query rows, so rank r is key tile r.  Invalid sequence bounds are skipped.
-template <int D>
-__global__ __launch_bounds__(256, (D == 64 ? 2 : 1)) void fa_bwd_dkdv_varlen_bf16_kernel(
-    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
-    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
-    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV,
-    const int *__restrict__ cu_seqlens, int n_seq, int total, int max_seqlen, int Hq, int Hkv,
-    float scale_log2, float scale) {
-  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
-  using P = DkvTile<D>;
-  const int per_rank = n_seq * Hkv;
-  const int kt = blockIdx.x / per_rank, rem = blockIdx.x - kt * per_rank;
-  const int s = rem / Hkv, hk = rem - s * Hkv;
-  const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
-  if (c0 < 0 || c1 < c0 || c1 > total) return;
-  const int T = min(c1 - c0, max_seqlen);  // the forward's clamp
-  if (kt >= (T + P::BNK - 1) / P::BNK) return;
-  const int G = Hq / Hkv;
-  const int64_t hs = (int64_t)total * D, kvb = (int64_t)hk * hs + (int64_t)c0 * D;
-  const int64_t q0 = (int64_t)hk * G;
-  const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs + (int64_t)c0 * D,
-                   dO + q0 * hs + (int64_t)c0 * D, LSE + q0 * total + c0,
-                   Delta + q0 * total + c0, hs, total, G, T};
-  dkdv_rows<D>(smem, hd, kt, scale_log2, scale);
-}
+// The batched and the packed variable-length dK/dV kernels at both head dims are the
+// generated stage streams of fa_bwd_dkdv64.hip and fa_bwd_dkdv128.hip (explicit
+// specializations declared in fa_bwd.h); their launchers are below.
 
 // 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): half the LDS and L2 bytes per
 // product, but half the workgroups and a longer prologue per workgroup, so only where its
@@ -635,7 +341,7 @@ template <int D>
 static hipError_t launch_dkdv(const void *q, const void *k, const void *v, const void *dout,
                               const float *lse, const float *delta, void *dk, void *dv, int B,
                               int Hq, int Hkv, int T, float scale, hipStream_t stream) {
-  const int n_ktiles = (T + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
+  const int n_ktiles = (T + 127) / 128;  // 128-key tiles
   constexpr size_t lds = D == 64 ? kDkv64LdsBytes : kDkv128LdsBytes;
   auto kern = fa_bwd_dkdv_bf16_kernel<D>;
   if (lds > 65536) {
@@ -677,8 +383,8 @@ static hipError_t launch_dkdv_varlen(const void *q, const void *k, const void *v
                                      void *dk, void *dv, const int *cu_seqlens, int n_seq,
                                      int total, int max_seqlen, int Hq, int Hkv, float scale,
                                      hipStream_t stream) {
-  const int max_ktiles = (max_seqlen + DkvTile<D>::BNK - 1) / DkvTile<D>::BNK;
-  constexpr size_t lds = DkvTile<D>::LDS_BYTES;
+  const int max_ktiles = (max_seqlen + 127) / 128;  // 128-key tiles
+  constexpr size_t lds = D == 64 ? kDkv64LdsBytes : kDkv128LdsBytes;
   auto kern = fa_bwd_dkdv_varlen_bf16_kernel<D>;
   if (lds > 65536) {
     hipError_t e = allow_lds<fa_bwd_dkdv_varlen_bf16_kernel<D>>(lds);

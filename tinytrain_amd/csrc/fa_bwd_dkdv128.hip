@@ -46,9 +46,9 @@ __device__ __forceinline__ void dkdv128_stage(f32x16 (&dk)[4], f32x16 (&dv)[4], 
 #undef TTFA_DKDV128_OPERANDS
 
 // D = 128: dK and dV for the 128 keys of key tile kt of one KV head, reduced over the
-// head's query-head group.  Same work split as dkdv_rows (4 waves x 32 keys, K/V rows in
-// registers, dK/dV accumulated over the group), with 128-row Q/dO stages double-buffered
-// through LDS and each stage's compute one hand-scheduled block per wave.  Ends with a
+// head's query-head group: 4 waves x 32 keys, the wave's K/V rows in registers, dK/dV
+// accumulated over the whole group in registers (no atomics), with 128-row Q/dO stages
+// double-buffered through LDS and each stage's compute one hand-scheduled block per wave.  Ends with a
 // workgroup barrier, so the caller may reuse the LDS ring right away.
 __device__ __forceinline__ void dkdv_rows128(bf16 *lds, const DkvHead &hd, int kt,
                                              float scale_log2, float scale) {
@@ -218,6 +218,38 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_bf16_kernel<128>(
     if (kt < 0) break;
     dkdv_rows128(smem, hd, kt, scale_log2, scale);
   }
+}
+
+// Packed variable-length sequences ([H, total, D] per tensor, sequence s at rows
+// cu_seqlens[s] .. cu_seqlens[s+1]-1 of every head): the same stage body per (key tile,
+// sequence, KV head), key-tile-major so every sequence's longest key tiles (tile 0 sees
+// all of its query rows) are dispatched first; a key tile past a sequence's end exits at
+// once.  Sequences whose bounds are not 0 <= cu[s] <= cu[s+1] <= total are skipped, and a
+// sequence longer than max_seqlen is processed as its first max_seqlen tokens (the
+// forward's clamp).  The per-sequence head view restricts every load to the sequence's
+// own rows (the buffer descriptors end at its last row).
+template <>
+__global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_varlen_bf16_kernel<128>(
+    const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
+    const bf16 *__restrict__ dO, const float *__restrict__ LSE,
+    const float *__restrict__ Delta, bf16 *__restrict__ dK, bf16 *__restrict__ dV,
+    const int *__restrict__ cu_seqlens, int n_seq, int total, int max_seqlen, int Hq, int Hkv,
+    float scale_log2, float scale) {
+  extern __shared__ __attribute__((aligned(16))) bf16 smem[];
+  const int per_rank = n_seq * Hkv;
+  const int kt = blockIdx.x / per_rank, rem = blockIdx.x - kt * per_rank;
+  const int s = rem / Hkv, hk = rem - s * Hkv;
+  const int c0 = cu_seqlens[s], c1 = cu_seqlens[s + 1];
+  if (c0 < 0 || c1 < c0 || c1 > total) return;
+  const int T = min(c1 - c0, max_seqlen);
+  if (kt >= (T + 127) / 128) return;
+  const int G = Hq / Hkv;
+  const int64_t hs = (int64_t)total * 128, kvb = (int64_t)hk * hs + (int64_t)c0 * 128;
+  const int64_t q0 = (int64_t)hk * G;
+  const DkvHead hd{K + kvb, V + kvb, dK + kvb, dV + kvb, Q + q0 * hs + (int64_t)c0 * 128,
+                   dO + q0 * hs + (int64_t)c0 * 128, LSE + q0 * total + c0,
+                   Delta + q0 * total + c0, hs, total, G, T};
+  dkdv_rows128(smem, hd, kt, scale_log2, scale);
 }
 
 }  // namespace ttfa
