@@ -50,7 +50,9 @@ struct DqTile {
   static constexpr int KB = BN / 32;             // 32-key blocks per tile
   static constexpr int KK = D / 16, DB = D / 32, CH = D / 8;
   static constexpr int LOADS = BN * CH / 256;    // 16-byte loads per thread per K (or V) tile
-  static constexpr int LDS_BYTES = 2 * 2 * BN * D * 2;  // [stage][K|V] bf16
+  // [stage][K|V] bf16; at D = 64 then the row tile's dO (its Q shares stage 1 in the
+  // prologue), so both arrive as coalesced direct-to-LDS loads (dq_rows)
+  static constexpr int LDS_BYTES = 2 * 2 * BN * D * 2 + (D == 64 ? BM * D * 2 : 0);
 };
 
 // One key tile of the dQ pass for one wave, one 32-key block at a time.
@@ -189,14 +191,46 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   load_tile(n_kv - 1, 0);
   bf16x8 qf[KK], dof[KK];
   float dpart = 0.f;
+  if constexpr (D == 64) {
+    // The row tile's Q and dO go to LDS (stage 1 of the ring, free until the loop's first
+    // prefetch, and the 16 KB after the ring) in the coalesced direct-to-LDS form, beside
+    // the first K/V tile in stage 0; O stays a register load (it only feeds Delta).
+    const uint32_t qbytes = head_bytes - (uint32_t)(qt * BM * D * 2);
+    const auto rqt = make_rsrc(hd.q + (int64_t)qt * BM * D, qbytes);
+    const auto rdot = make_rsrc(hd.dout + (int64_t)qt * BM * D, qbytes);
+    bf16 *Qs = lds + 2 * BN * D, *dOs = lds + 4 * BN * D;
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2;
-    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
-    dof[kk] = __builtin_bit_cast(bf16x8, buf_load16(rdo, off));
-    const bf16x8 of = __builtin_bit_cast(bf16x8, buf_load16(ro, off));
+    for (int i = 0; i < BM * CH / 256; ++i) {
+      const int e = 256 * i + 64 * wave + lane, row = e / CH, pc = e % CH;
+      const uint32_t off = (uint32_t)(row * D + swz_l<D, kDqLayout>(row, pc) * 8) * 2;
+      buf_load16_lds(rqt, off, Qs + (256 * i + 64 * wave_s) * 8);
+      buf_load16_lds(rdot, off, dOs + (256 * i + 64 * wave_s) * 8);
+    }
+    bf16x8 of[KK];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[s]), bf2f(dof[kk][s]), dpart);
+    for (int kk = 0; kk < KK; ++kk)
+      of[kk] = __builtin_bit_cast(bf16x8, buf_load16(ro, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      qf[kk] = lds_read_row8<D, kDqLayout>(Qs, wave * 32 + lq, 2 * kk + lg);
+      dof[kk] = lds_read_row8<D, kDqLayout>(dOs, wave * 32 + lq, 2 * kk + lg);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[kk][s]), bf2f(dof[kk][s]), dpart);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's Q / dO reads are complete
+    __syncthreads();                     // ... in every wave, before stage 1 is refilled
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const uint32_t off = (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2;
+      qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, off));
+      dof[kk] = __builtin_bit_cast(bf16x8, buf_load16(rdo, off));
+      const bf16x8 of = __builtin_bit_cast(bf16x8, buf_load16(ro, off));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) dpart = __builtin_fmaf(bf2f(of[s]), bf2f(dof[kk][s]), dpart);
+    }
   }
   const float delta = xhalf_sum(dpart);
   float lse_t = 0.f;

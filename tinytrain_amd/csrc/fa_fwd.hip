@@ -169,7 +169,6 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
   const int qrow = q0 + lq;
 
   const uint32_t head_bytes = (uint32_t)T * D * 2;
-  const auto rq = make_rsrc(hd.q, head_bytes);
 
   // Global -> LDS without registers: the wave fills 1 KB blocks of the swizzled tile;
   // lane l of block e0 writes physical chunk (e0 + l) % CH of row (e0 + l) / CH, which
@@ -197,15 +196,29 @@ __device__ __forceinline__ void fwd_rows(bf16 (*lds)[2][FwdTile<D>::BN * D], con
   };
 
   // Q^T as B operand: lane (lq, lg) slot s of step kk holds Q[qrow][16kk + 8lg + s].
+  // The row tile's Q goes to LDS stage 1 (free until the loop's first prefetch) in the
+  // coalesced direct-to-LDS form, beside the first K/V tile in stage 0, and each wave
+  // reads its fragments from there.
+  load_tile(0, 0);
+  {
+    const uint32_t qbytes = head_bytes - (uint32_t)(qt * BM * D * 2);
+    const auto rqt = make_rsrc(hd.q + (int64_t)qt * BM * D, qbytes);
+    bf16 *Qs = &lds[1][0][0];  // 128 rows x D across stage 1's K and V halves
+#pragma unroll
+    for (int i = 0; i < 2 * LOADS; ++i) {
+      const int e = 256 * i + 64 * wave + lane, row = e / CH, pc = e % CH;
+      const uint32_t off = (uint32_t)(row * D + swz_l<D, kFwdLayout>(row, pc) * 8) * 2;
+      buf_load16_lds(rqt, off, Qs + (256 * i + 64 * wave_s) * 8);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
   bf16x8 qf[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
-    qf[kk] = __builtin_bit_cast(bf16x8, buf_load16(rq, (uint32_t)(qrow * D + 16 * kk + 8 * lg) * 2));
-  load_tile(0, 0);
-  // Every load issued so far (Q and the first tile) is complete here, so the loop body
-  // never waits on the Q registers behind the next tile's prefetch.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
+    qf[kk] = lds_read_row8<D, kFwdLayout>(&lds[1][0][0], wave * 32 + lq, 2 * kk + lg);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's Q reads are complete
+  __syncthreads();                     // ... in every wave, before stage 1 is refilled
 
   const int n_kv = min((T + BN - 1) / BN, (qt + 1) * (BM / BN));
   // Tiles [0, n_full) are visible to every row of this wave and lie inside T;
