@@ -6,7 +6,9 @@
   that see no key: O = 0, LSE = -inf), 1, and the full cache;
 * decoding the last rows of a sequence agrees with the batched forward kernel on the
   whole sequence;
-* run-to-run bitwise determinism and the torch.library op checks.
+* run-to-run bitwise determinism and the torch.library op checks;
+* a workspace reused across shapes with leftovers in it, and HIP-graph replays with new
+  inputs, both bitwise equal to fresh eager calls.
 """
 
 import pytest
@@ -107,3 +109,67 @@ def test_decode_deterministic_and_opcheck():
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
     torch.library.opcheck(flash_attn_decode, (q, k, v, lens),
                           test_utils=("test_schema", "test_faketensor"))
+
+
+def test_decode_shared_workspace_with_leftovers():
+    """One workspace reused by calls of different shapes through the C ABI, first filled
+    with random bits: every call equals a call of the op on a fresh workspace, bitwise
+    (nothing a call reads from the workspace was left there by another)."""
+    import math
+
+    from tinytrain_amd import _lib
+
+    announce("decode shared workspace with leftovers")
+    lib = _lib.load()
+    shapes = [(1, 16, 8, 1, 16384, 128, [16384]), (4, 8, 2, 2, 1024, 64, [1024, 700, 3, 1]),
+              (128, 16, 8, 1, 1024, 128, None), (2, 12, 12, 1, 5000, 64, [4999, 2048])]
+    need = max(lib.ttfa_decode_workspace_bytes(B, Hq, Hkv, Tq, L, D)
+               for B, Hq, Hkv, Tq, L, D, _ in shapes)
+    ws = torch.randint(-2**62, 2**62, (need // 8 + 2,), dtype=torch.int64, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for rep in range(2):
+        for i, (B, Hq, Hkv, Tq, L, D, lens) in enumerate(shapes):
+            q, k, v = (t.to(DEV) for t in _inputs(B, Hq, Hkv, Tq, L, D, seed=10 * i + rep))
+            if lens is None:
+                lens = [L - 7 * j for j in range(B)]
+            lens_t = torch.tensor(lens, dtype=torch.int32, device=DEV)
+            want_o, want_lse = flash_attn_decode(q, k, v, lens_t)
+            o, lse = torch.empty_like(q), torch.empty(B, Hq, Tq, device=DEV)
+            _lib.check(lib.ttfa_decode_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                           lens_t.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                           ws.data_ptr(), B, Hq, Hkv, Tq, L, D, _lib.TTFA_BF16,
+                                           1.0 / math.sqrt(D), stream))
+            torch.cuda.synchronize()
+            assert torch.equal(o, want_o), (rep, i)
+            assert torch.equal(lse, want_lse), (rep, i)
+
+
+def test_decode_graph_replays():
+    """flash_attn_decode captured in a HIP graph (16 key splits per row) and replayed with
+    new cache contents and lengths between the replays (eager work and synchronisations in
+    between): each replay equals the eager op on the same inputs, bitwise."""
+    announce("decode graph replays")
+    B, Hq, Hkv, Tq, L, D = 2, 16, 8, 1, 8192, 128
+    q_s, k_s, v_s = (t.to(DEV) for t in _inputs(B, Hq, Hkv, Tq, L, D, seed=20))
+    lens_s = torch.tensor([L, 5000], dtype=torch.int32, device=DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        flash_attn_decode(q_s, k_s, v_s, lens_s)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        o_s, lse_s = flash_attn_decode(q_s, k_s, v_s, lens_s)
+    for r in range(4):
+        q, k, v = (t.to(DEV) for t in _inputs(B, Hq, Hkv, Tq, L, D, seed=21 + r))
+        q_s.copy_(q)
+        k_s.copy_(k)
+        v_s.copy_(v)
+        lens_s.copy_(torch.tensor([L - 100 * r, 3000 + 7 * r], dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        want_o, want_lse = flash_attn_decode(q_s, k_s, v_s, lens_s)
+        torch.cuda.synchronize()
+        assert torch.equal(o_s, want_o), r
+        assert torch.equal(lse_s, want_lse), r
