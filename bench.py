@@ -610,6 +610,21 @@ class HipTimingEvent:
             self._hip.hipEventDestroy(self._e)
 
 
+def _settle(fn, ms: float) -> dict:
+    """Untimed calls of ``fn`` in chunks of 8 until ``ms`` of wall time has passed, so the
+    timed calls that follow run at the clocks a loaded GPU settles to (as the main bench's
+    settle phase); returns the ``settle`` field of the line."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while ms > 0 and (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+    return {"calls": n, "seconds": round(time.perf_counter() - t0, 3)}
+
+
 def _ev_time(fn, steps: int, warmup: int) -> float:
     """Median ms of ``fn`` over ``steps`` calls (timing-only HIP events on the current
     stream around each call)."""
@@ -628,7 +643,7 @@ def _ev_time(fn, steps: int, warmup: int) -> float:
     return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
 
 
-def _prologue_bench(dev, steps: int, warmup: int) -> int:
+def _prologue_bench(dev, steps: int, warmup: int, settle_ms: float = 0.0) -> int:
     """Fused q/k norm + RoPE + layout op vs the eager expressions it replaces
     (model.py:83-93), forward and backward, at the reference model's attention inputs
     (B=32, T=512, Hq=8, Hkv=2, D=128, bf16).  The op is HBM-bound: its roofline is the
@@ -651,6 +666,9 @@ def _prologue_bench(dev, steps: int, warmup: int) -> int:
 
     out = qk_norm_rope_fwd(q, k, v, wq, wk, cos, sin, eps)
     rq, rk = out[3], out[4]
+    settle = _settle(lambda: (qk_norm_rope_fwd(q, k, v, wq, wk, cos, sin, eps),
+                              qk_norm_rope_bwd(gq, gk, gk, q, k, wq, wk, cos, sin, rq, rk)),
+                     settle_ms)
     op_fwd = _ev_time(lambda: qk_norm_rope_fwd(q, k, v, wq, wk, cos, sin, eps), steps, warmup)
     op_bwd = _ev_time(lambda: qk_norm_rope_bwd(gq, gk, gk, q, k, wq, wk, cos, sin, rq, rk),
                       steps, warmup)
@@ -725,12 +743,13 @@ def _prologue_bench(dev, steps: int, warmup: int) -> int:
             "bwd": {"bytes": bwd_bytes, "achieved": round(bwd_bytes / fused_bwd / 1e6, 1),
                     "frac": round(bwd_bytes / fused_bwd / 1e6 / peak, 4)},
         },
+        "settle": settle,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def _varlen_bench(dev, steps: int, warmup: int) -> int:
+def _varlen_bench(dev, steps: int, warmup: int, settle_ms: float = 0.0) -> int:
     """Packed variable-length causal attention at C2's head shape (Hq = Hkv = 12, D = 64)
     and token count (16 x 1024): seeded lengths 64..2048, fwd and bwd through the C ABI,
     algorithmic FLOPs summed per sequence (2 * Hq * len^2 * D forward, x2.5 backward)."""
@@ -769,6 +788,7 @@ def _varlen_bench(dev, steps: int, warmup: int) -> int:
                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *args))
 
     fwd()
+    settle = _settle(lambda: (fwd(), bwd()), settle_ms)
     f_ms, b_ms = _ev_time(fwd, steps, warmup), _ev_time(bwd, steps, warmup)
     fwd_flop = sum(2.0 * Hq * L * L * D for L in lens)
     line = {
@@ -780,12 +800,13 @@ def _varlen_bench(dev, steps: int, warmup: int) -> int:
         "bwd": {"ms": round(b_ms, 4), "tflops": round(2.5 * fwd_flop / b_ms / 1e9, 1)},
         "fwd_bwd_tflops": round(3.5 * fwd_flop / (f_ms + b_ms) / 1e9, 1),
         "frac_of_peak": round(3.5 * fwd_flop / (f_ms + b_ms) / 1e9 / PEAK_BF16_TFLOPS, 4),
+        "settle": settle,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def _decode_bench(dev, steps: int, warmup: int) -> int:
+def _decode_bench(dev, steps: int, warmup: int, settle_ms: float = 0.0) -> int:
     """KV-cache decode (one new token per sequence) at the C4/C5 head shape (Hq 16,
     Hkv 8, D 128): a rollout-sized batch (B 32, caches of 4096) and one long sequence
     (B 1, 16384).  HBM-bound: the roofline is the cache bytes read (K and V of every
@@ -813,6 +834,7 @@ def _decode_bench(dev, steps: int, warmup: int) -> int:
                                            ws.data_ptr(), B, Hq, Hkv, Tq, L, D, _lib.TTFA_BF16,
                                            1.0 / math.sqrt(D), sp))
 
+        settle = _settle(call, settle_ms if not out else 0.0)  # once, before the first case
         ms = _ev_time(call, steps, warmup)
         # the same calls back to back, timed as one block: the launches queue ahead of the
         # GPU, so no host time falls between them (per-call events expose it when a call
@@ -833,7 +855,8 @@ def _decode_bench(dev, steps: int, warmup: int) -> int:
                     "frac_of_hbm_peak": round(nbytes / ms / 1e6 / 8000.0, 4),
                     "ms_back_to_back": round(ms_b2b, 4),
                     "GB_per_s_back_to_back": round(nbytes / ms_b2b / 1e6, 1),
-                    "frac_of_hbm_peak_back_to_back": round(nbytes / ms_b2b / 1e6 / 8000.0, 4)})
+                    "frac_of_hbm_peak_back_to_back": round(nbytes / ms_b2b / 1e6 / 8000.0, 4),
+                    **({"settle": settle} if settle["calls"] else {})})
     print(json.dumps({"metric": "KV-cache decode attention, HBM GB/s (split + merge launches)",
                       "roofline": {"bound": "hbm", "peak": 8000.0, "unit": "GB/s"},
                       "timing": "ms: median of timing-only events around each call (includes the "
@@ -998,11 +1021,11 @@ def main() -> int:
     if args.copy_probe_mb > 0:
         return _copy_probe(args.copy_probe_mb, args.steps, dev)
     if args.prologue:
-        return _prologue_bench(dev, args.steps, args.warmup)
+        return _prologue_bench(dev, args.steps, args.warmup, args.settle_ms)
     if args.varlen:
-        return _varlen_bench(dev, args.steps, args.warmup)
+        return _varlen_bench(dev, args.steps, args.warmup, args.settle_ms)
     if args.decode:
-        return _decode_bench(dev, args.steps, args.warmup)
+        return _decode_bench(dev, args.steps, args.warmup, args.settle_ms)
     if args.model:
         return _model_bench(dev, min(args.steps, 20), min(max(args.warmup, 3), 5),
                             args.model_batch)
