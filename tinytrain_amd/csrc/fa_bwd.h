@@ -33,8 +33,7 @@ __global__ void fa_bwd_dq_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__
                                       const bf16 *__restrict__ V, const bf16 *__restrict__ O,
                                       const bf16 *__restrict__ dO, const float *__restrict__ LSE,
                                       float *__restrict__ Delta, bf16 *__restrict__ dQ, int B,
-                                      int Hq, int Hkv, int T, float scale_log2, float scale,
-                                      int paired);
+                                      int Hq, int Hkv, int T, float scale_log2, float scale);
 // D = 128 dQ pass over 256-row tiles, 64 rows per wave (fa_bwd_dq128.hip): for launches
 // whose 256-row pairs fill the resident workgroup slots and whose T exceeds 1792.
 __global__ void fa_bwd_dq_wide_bf16_kernel(const bf16 *__restrict__ Q, const bf16 *__restrict__ K,

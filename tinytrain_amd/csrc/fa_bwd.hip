@@ -4,12 +4,11 @@
 // :208-209) instead of storing it:
 //
 //  1. dQ pass (reference: bwd_preprocess :70-90 fused with bwd_dq_kernel :162-217).
-//     A row tile = 128 query rows of one (batch, head), 4 waves x 32 rows.  At D = 128
-//     a workgroup takes a balanced pair of row tiles, the longer first (pair_item), when
-//     pairs fill whole rounds of the resident slots; at D = 64 it takes one row tile,
-//     longest first, so the row body is inlined once and three workgroups per CU fit
-//     without spills.  Key tiles run from the row tile's diagonal down to key 0.  (Long
-//     sequences at D = 128 take the 256-row pass of fa_bwd_dq128.hip.)
+//     A row tile = 128 query rows of one (batch, head), 4 waves x 32 rows.  A workgroup
+//     takes one row tile, longest first (single_item), so the row body is inlined once
+//     (three workgroups per CU fit without spills at D = 64).  Key tiles run from the row
+//     tile's diagonal down to key 0.  (Long sequences at D = 128 take the 256-row pass of
+//     fa_bwd_dq128.hip.)
 //     The prologue computes Delta = rowsum(O * dO) for the tile's own rows from the
 //     same registers that hold dO, and writes it to the workspace
 //     for pass 2 (so there is no separate preprocess launch and dO is read once here).
@@ -141,9 +140,9 @@ __device__ __forceinline__ void dq_rows(bf16 *lds, const DqHead &hd, int qt, flo
   constexpr int BM = P::BM, BN = P::BN, KK = P::KK, DB = P::DB, CH = P::CH, LOADS = P::LOADS;
   const int T = hd.T;
 
-  // An opaque copy of the thread id: the batched kernel at D = 128 inlines this body
-  // twice (paired row tiles), and without it the compiler shares lane-derived addresses
-  // between the two copies, which keeps them live across the first.
+  // An opaque copy of the thread id: values derived from it are computed once and kept,
+  // not rematerialised from threadIdx; without it the compiler's allocation of the D = 64
+  // kernels spills (8 bytes of scratch; the asm contract test checks for spills).
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const int wave = tid >> 6, lane = tid & 63;
@@ -278,21 +277,21 @@ __global__ __launch_bounds__(256, (D == 64 ? 3 : 2)) void fa_bwd_dq_bf16_kernel(
     const bf16 *__restrict__ Q, const bf16 *__restrict__ K, const bf16 *__restrict__ V,
     const bf16 *__restrict__ O, const bf16 *__restrict__ dO, const float *__restrict__ LSE,
     float *__restrict__ Delta, bf16 *__restrict__ dQ, int B, int Hq, int Hkv, int T,
-    float scale_log2, float scale, int paired) {
+    float scale_log2, float scale) {
   extern __shared__ __attribute__((aligned(16))) bf16 smem[];  // [stage 2][K|V][BN*D]
   using P = DqTile<D>;
   const int n_tiles = (T + P::BM - 1) / P::BM;
-  const WorkPair w = sched_item(paired, blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
+  // One row tile per workgroup, longest first.  Pairs of row tiles (the forward's
+  // schedule) would need a second inlined copy of the row body, which at D = 64 does not
+  // fit three workgroups per CU without spills; at D = 128 (two per CU) longest-first
+  // single tiles measured 0-4% faster than pairs at T = 500-1536.
+  const WorkPair w = single_item(blockIdx.x, n_tiles, B, Hq, Hq / Hkv, false);
   const int G = Hq / Hkv;
   const int b = w.bh / Hq, h = w.bh - b * Hq;
   const int64_t kvh = (int64_t)b * Hkv + h / G, hs = (int64_t)T * D, qb = w.bh * hs;
   const DqHead hd{Q + qb, K + kvh * hs, V + kvh * hs, O + qb, dO + qb,
                   LSE + (int64_t)w.bh * T, Delta + (int64_t)w.bh * T, dQ + qb, T};
   dq_rows<D>(smem, hd, w.first, scale_log2, scale);
-  // D = 64 runs single tiles only (the launcher never pairs it): a second inlined copy of
-  // the row body would not fit three workgroups per CU without spills, and the spill
-  // reloads wait on the tile prefetch.  Longest-first singles balance as well here.
-  if (D != 64 && w.second >= 0) dq_rows<D>(smem, hd, w.second, scale_log2, scale);
 }
 
 // Packed variable-length sequences ([H, total, D], sequence s at rows cu_seqlens[s] ..
@@ -362,12 +361,10 @@ static hipError_t launch_dq(const void *q, const void *k, const void *v, const v
     hipError_t e = allow_lds<fa_bwd_dq_bf16_kernel<D>>(lds);
     if (e != hipSuccess) return e;
   }
-  const bool paired =
-      D != 64 && use_pairs(n_tiles, B, Hq, resident_slots<fa_bwd_dq_bf16_kernel<D>>(256, lds));
-  const dim3 grid((unsigned)sched_items(paired, n_tiles, B, Hq)), block(256);
+  const dim3 grid((unsigned)sched_items(false, n_tiles, B, Hq)), block(256);
   kern<<<grid, block, lds, stream>>>((const bf16 *)q, (const bf16 *)k, (const bf16 *)v,
                                      (const bf16 *)o, (const bf16 *)dout, lse, delta, (bf16 *)dq,
-                                     B, Hq, Hkv, T, scale * kLog2e, scale, (int)paired);
+                                     B, Hq, Hkv, T, scale * kLog2e, scale);
   return hipGetLastError();
 }
 
