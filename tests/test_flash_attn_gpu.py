@@ -3,8 +3,8 @@
 Ports the reference's GPU test file (tests/test_flash_attn.py of tinytrain: parity vs
 fp32 SDPA at its three shapes, opcheck, autograd == launcher bitwise, compile
 fullgraph, whole-model logits) and adds the five workload configurations at full size,
-ragged / tiny / odd-group edge cases, unwritten-output poisoning and run-to-run
-determinism.  Every comparison is against the oracle on the CPU, on the same seeded
+ragged / tiny / odd-group / long-row (T up to 6000 at D=64) edge cases, unwritten-output
+poisoning and run-to-run determinism.  Every comparison is against the oracle on the CPU, on the same seeded
 bits (inputs are drawn on the CPU and copied over).
 """
 
@@ -145,6 +145,8 @@ def test_wide_d128_kernels(B, H, H_kv, T):
     (1, 4, 2, 500, 64, torch.bfloat16),
     (1, 6, 2, 1000, 128, torch.bfloat16),
     (3, 2, 2, 64, 128, torch.bfloat16),    # exactly one KV tile
+    (1, 2, 1, 6000, 64, torch.bfloat16),   # long rows at D=64 (47 row tiles), G=2, ragged
+    (1, 2, 2, 4097, 64, torch.bfloat16),   # one row past a 128-row tile at long T
     (1, 1, 1, 1, 128, torch.float32),
     (1, 2, 1, 33, 128, torch.float32),
     (2, 4, 2, 100, 64, torch.float32),
