@@ -1188,6 +1188,11 @@ def main() -> int:
                 launch(sets[i])
         launch_sp[0] = sp
         reps = max(1, K // gsets)
+        # The capture leaves the GPU idle for milliseconds, after which its clocks take
+        # longer than the few replays below to come back (measured: the same kernels ~20%
+        # slower for 40 steps after a 50 ms pause, eager or replayed alike), so replays
+        # run for --settle-ms first, as the timed region's own settle phase does.
+        graph_settle = _settle(graph.replay, args.settle_ms)
         for _ in range(2):
             graph.replay()
         gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -1261,9 +1266,11 @@ def main() -> int:
         },
         "graph_replay": None if graph_ms is None else {
             "note": "the same launches captured in one HIP graph (one step per input set, "
-                    "up to 8 sets) and replayed: the step without per-call host overhead",
+                    "up to 8 sets) and replayed after replays for --settle-ms: the step "
+                    "without per-call host overhead",
             "ms_per_step": round(graph_ms, 5),
             "fwd_bwd_tflops": round(3.5 * fwd_f / (graph_ms * 1e-3) / 1e12, 2),
+            "settle": graph_settle,
         },
         "roofline": {
             "bound": "mfma",
