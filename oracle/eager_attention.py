@@ -16,6 +16,9 @@ What it restates (reference = XinqiWan412/tinytrain, files under /root/reference
   ``O = softmax(s) v`` (:55-63) and ``LSE = m + ln(l)`` in natural-log units of the
   scaled scores, fp32, shape [B, Hq, T] (:67, :232).
 * ``attention_delta``      -- ``Delta = rowsum(O * dO)`` (kernels/flash_attn.py:70-90).
+* ``attention_bwd_rows`` / ``attention_bwd_keys`` -- the same formulas for sampled query
+  rows (dQ) or keys (dK, dV) only, each from its own row or column of scores, for lengths
+  where the full backward is too slow on the CPU.
 * ``attention_bwd``        -- the backward formulas of kernels/flash_attn.py:93-217:
   ``P = exp(s*scale - LSE)`` (:143-145), ``dV = P^T dO`` (:147), ``dP = dO V^T`` (:149),
   ``dS = P (dP - Delta)`` (:150), ``dK = dS^T Q * scale`` (:152-154),
@@ -33,6 +36,8 @@ How each function is pinned (tests/test_oracle.py):
 * ``attention_bwd`` vs autograd through ``eager_attention`` (SDPA backward), and vs
   ``torch.autograd.gradcheck`` finite differences of ``attention_fwd`` in fp64, which
   fixes every gradient formula independently of how it is written here.
+* ``attention_bwd_rows`` / ``attention_bwd_keys`` vs ``attention_bwd`` on every row and key
+  of small GQA inputs, and a planted missing Delta in the key form is caught.
 * GQA: result equals running with k/v expanded by ``repeat_interleave``, with dK/dV
   equal to the group sum of the expanded gradients (tests/test_model.py:174-200).
 * A brute-force scalar pure-Python loop on tiny inputs (``brute_force_attention``).
@@ -163,6 +168,51 @@ def attention_bwd(q: Tensor, k: Tensor, v: Tensor, o: Tensor, do: Tensor, lse: T
     dk = dke.view(B, Hkv, g, T, D).sum(dim=2)
     dv = dve.view(B, Hkv, g, T, D).sum(dim=2)
     return dq, dk, dv
+
+
+def attention_bwd_rows(q: Tensor, k: Tensor, v: Tensor, do: Tensor, o: Tensor, lse: Tensor,
+                       b: int, h: int, rows, scale: Optional[float] = None) -> Tensor:
+    """dQ of the given query rows of (batch b, query head h), in fp64, from each row's own
+    scores only (kernels/flash_attn.py:196-216): dQ_i = scale * sum_{j<=i} P_ij (dP_ij - Delta_i)
+    K_j with P_ij = exp(s_ij - LSE_i), dP_ij = dO_i . V_j, Delta_i = O_i . dO_i.  ``o`` and
+    ``lse`` are the forward's outputs for every row.  Returns [len(rows), D]."""
+    D = q.shape[-1]
+    g = _group(q, k)
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    out = []
+    for i in rows:
+        K, V = k[b, h // g, :i + 1].double(), v[b, h // g, :i + 1].double()
+        dor = do[b, h, i].double()
+        p = torch.exp((K @ q[b, h, i].double()) * scale - lse[b, h, i].double())
+        delta = (o[b, h, i].double() * dor).sum()
+        out.append(((p * (V @ dor - delta))[:, None] * K).sum(0) * scale)
+    return torch.stack(out)
+
+
+def attention_bwd_keys(q: Tensor, k: Tensor, v: Tensor, do: Tensor, o: Tensor, lse: Tensor,
+                       b: int, hk: int, keys, scale: Optional[float] = None
+                       ) -> Tuple[Tensor, Tensor]:
+    """dK and dV of the given keys of (batch b, KV head hk), in fp64, from each key's own
+    column of scores over the rows i >= j, summed over the KV head's query heads
+    (kernels/flash_attn.py:121-159): dV_j = sum P_ij dO_i, dK_j = scale * sum P_ij
+    (dP_ij - Delta_i) Q_i.  Returns ([len(keys), D], [len(keys), D])."""
+    D = q.shape[-1]
+    g = _group(q, k)
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    dks, dvs = [], []
+    for j in keys:
+        dk = torch.zeros(D, dtype=torch.float64)
+        dv = torch.zeros(D, dtype=torch.float64)
+        kj, vj = k[b, hk, j].double(), v[b, hk, j].double()
+        for h in range(hk * g, (hk + 1) * g):
+            Q, dO = q[b, h, j:].double(), do[b, h, j:].double()
+            p = torch.exp((Q @ kj) * scale - lse[b, h, j:].double())
+            delta = (o[b, h, j:].double() * dO).sum(-1)
+            dv += (p[:, None] * dO).sum(0)
+            dk += ((p * (dO @ vj - delta))[:, None] * Q).sum(0) * scale
+        dks.append(dk)
+        dvs.append(dv)
+    return torch.stack(dks), torch.stack(dvs)
 
 
 def brute_force_attention(q, k, v):

@@ -13,7 +13,8 @@ import math
 import pytest
 import torch
 
-from oracle.eager_attention import (attention_bwd, attention_delta, attention_fwd,
+from oracle.eager_attention import (attention_bwd, attention_bwd_keys, attention_bwd_rows,
+                                    attention_delta, attention_fwd,
                                     brute_force_attention, eager_attention,
                                     eager_attention_grads, max_abs, reference_outputs,
                                     varlen_reference)
@@ -173,6 +174,31 @@ def test_planted_swapped_kv_is_caught():
     q, k, v, _ = _rand(1, 2, 2, 20, 64, seed=15)
     o_bad, _ = attention_fwd(q, v, k)
     assert max_abs(o_bad, eager_attention(q, k, v)) > 1e-2
+
+
+@pytest.mark.parametrize("Hq, Hkv, T, D", [(4, 2, 45, 64), (3, 1, 33, 128)])
+def test_sampled_rows_and_keys_match_full_backward(Hq, Hkv, T, D):
+    """The per-row dQ and per-key dK / dV forms (used where the full backward is too
+    slow) equal the full backward on every row and key, GQA included."""
+    q, k, v, do = _rand(2, Hq, Hkv, T, D, seed=21)
+    o, lse = attention_fwd(q, k, v)
+    dq, dk, dv = attention_bwd(q, k, v, o, do, lse)
+    for b in range(2):
+        for h in range(Hq):
+            got = attention_bwd_rows(q, k, v, do, o, lse, b, h, range(T))
+            assert max_abs(got, dq[b, h]) < 1e-10
+        for hk in range(Hkv):
+            gk, gv = attention_bwd_keys(q, k, v, do, o, lse, b, hk, range(T))
+            assert max_abs(gk, dk[b, hk]) < 1e-10
+            assert max_abs(gv, dv[b, hk]) < 1e-10
+
+
+def test_planted_dropped_delta_in_key_form_is_caught():
+    q, k, v, do = _rand(1, 2, 1, 30, 64, seed=22)
+    o, lse = attention_fwd(q, k, v)
+    _, dk, _ = attention_bwd(q, k, v, o, do, lse)
+    bad, _ = attention_bwd_keys(q, k, v, do, torch.zeros_like(o), lse, 0, 0, range(30))
+    assert max_abs(bad, dk[0, 0]) > 1e-3
 
 
 # ------------------------------------------------------- seeded workload inputs
