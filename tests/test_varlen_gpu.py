@@ -6,7 +6,8 @@ and the CPU oracle.
   same arithmetic, only the work-item mapping differs;
 * the packed result matches oracle.eager_attention.varlen_reference (block-diagonal
   causal attention, fp32) within the attention tolerances;
-* empty sequences, length-1 sequences, tile-boundary lengths, GQA, both head dims;
+* empty sequences, length-1 sequences, tile-boundary lengths, a 4500-token sequence, GQA,
+  both head dims;
   rows of sequences with invalid bounds are left unwritten; opcheck and autograd.
 """
 
@@ -26,6 +27,9 @@ CASES = [
     ([1, 127, 128, 129, 300, 64], 8, 2, 64),
     ([5, 0, 256, 1000, 3], 4, 4, 128),
     ([513, 77], 16, 8, 128),
+    # long rows at D = 64 (the batched kernels there have no 256-row form, so bitwise
+    # equality to the per-sequence launch holds at any length)
+    ([4500, 1, 2047, 129], 4, 2, 64),
 ]
 
 
